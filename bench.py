@@ -1,0 +1,357 @@
+"""Benchmark of the MelBandRoformer tensor-op hot path on one MI355X.
+
+One step = one pass of every BASELINE op at its full chunk shape (BL-1 .. BL-5), each
+on synthetic inputs already resident in HBM:
+  BL-1  residual add + RMSNorm f32 [48060, 384] (writes the sum and the normed rows)
+  BL-2  GELU bf16 [48060, 1536]; GLU bf16 [48060, 3072]; sigmoid gate x head merge bf16
+        attn [60, 8, 801, 64] + logits [48060, 8]
+  BL-3  row softmax, f32 and bf16: time [480*801, 801] and freq [6408*60, 60]
+  BL-4  rotary in place bf16 q, k [480, 801, 64] with f32 cos/sin [801, 32];
+        permute bf16 [4, 801, 60, 384] -> [4, 60, 801, 384] and back
+  BL-5  band gather and mask merge, batch 4, 60 mel bands (3958 stereo band-bins)
+value = sum of algorithmic bytes / sum of op times (GB/s, all ops); per-op GB/s and the
+fraction of the 8 TB/s HBM peak are in config.per_op.  Op times are HIP events recorded
+on the stream the kernels run on.  Each op cycles through enough buffer sets that the
+working set between two uses of a set exceeds 1 GB, so the 256 MB MALL cannot serve
+repeats.  Algorithmic bytes count every input read once and every output written once.
+
+cpu_baseline: the oracle's float pipeline (oracle/, OpenMP) on a row sample of every op,
+timed on this host's cores.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "mbr-cuda-tile_amd"))
+
+METRIC = "achieved HBM GB/s (% of MI355X peak) per op; ms of tensor ops per chunk"
+HBM_PEAK_GBS = 8000.0
+MALL_DEFEAT_BYTES = 1.1e9
+TRAFFIC_SUMMARY = REPO / "profiles" / "traffic_softmax_time_f32.md"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-threads", type=int, default=None)
+    return ap.parse_args()
+
+
+class Op:
+    def __init__(self, name, nbytes, make, kernel):
+        self.name = name
+        self.bytes = nbytes      # algorithmic bytes per call
+        self.make = make         # () -> buffer set (dict)
+        self.kernel = kernel     # kernel symbol substring (for the rocprof cross-check)
+        self.sets = []
+        self.run = None          # (buffer set) -> None
+        self.times_ms = []
+
+
+def build_ops(torch, mbrt, bands):
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0x4D42520000)
+
+    def randn(shape, dtype=torch.float32, std=1.0, mean=0.0):
+        return (torch.randn(shape, generator=g, device=dev) * std + mean).to(dtype)
+
+    bf16, f32 = torch.bfloat16, torch.float32
+    ops = []
+
+    # BL-1 residual + RMSNorm f32
+    R, D = 48060, 384
+    gamma = randn((D,), mean=1.0, std=0.02)
+    op = Op("bl1_residual_rmsnorm_f32", 4 * R * D * 4 + D * 4,
+            lambda: dict(x=randn((R, D)), r=randn((R, D)), s=torch.empty((R, D), device=dev),
+                         y=torch.empty((R, D), device=dev)), "rms_fast_kernel")
+    op.run = lambda b: mbrt.residual_add_rms_norm(b["x"], b["r"], gamma, b["s"], b["y"], math.sqrt(D), 1e-8)
+    ops.append(op)
+
+    # BL-2a GELU bf16
+    op = Op("bl2a_gelu_bf16", 2 * 48060 * 1536 * 2,
+            lambda: dict(x=randn((48060, 1536), bf16, 1.5), y=torch.empty((48060, 1536), dtype=bf16, device=dev)),
+            "bias_act_vec_kernel")
+    op.run = lambda b: mbrt.bias_act(b["x"], None, b["y"], mbrt.ACT_GELU_REF)
+    ops.append(op)
+
+    # BL-2b GLU bf16
+    op = Op("bl2b_glu_bf16", 48060 * 3072 * 2 + 48060 * 1536 * 2,
+            lambda: dict(x=randn((48060, 3072), bf16, 1.5), y=torch.empty((48060, 1536), dtype=bf16, device=dev)),
+            "glu_vec_kernel")
+    op.run = lambda b: mbrt.glu(b["x"], b["y"])
+    ops.append(op)
+
+    # BL-2c sigmoid gate x head merge bf16, attention output head-major [B, H, N, D]
+    B, H, N, Dh = 60, 8, 801, 64
+    op = Op("bl2c_gate_merge_bf16", 2 * B * H * N * Dh * 2 + B * N * H * 2,
+            lambda: dict(a=randn((B, H, N, Dh), bf16), gl=randn((B, N, H), bf16, 2.0),
+                         y=torch.empty((B, N, H * Dh), dtype=bf16, device=dev)), "gate_merge_vec_kernel")
+    op.run = lambda b: mbrt.gate_merge(b["a"], b["gl"], b["y"], mbrt.LAYOUT_BHND)
+    ops.append(op)
+
+    # BL-3 softmax
+    for tag, rows, cols in (("time", 480 * 801, 801), ("freq", 6408 * 60, 60)):
+        for dt, dname in ((f32, "f32"), (bf16, "bf16")):
+            es = 4 if dt == f32 else 2
+            op = Op(f"bl3_softmax_{tag}_{dname}", 2 * rows * cols * es,
+                    (lambda rows=rows, cols=cols, dt=dt: dict(x=randn((rows, cols), dt, 3.0),
+                                                              y=torch.empty((rows, cols), dtype=dt, device=dev))),
+                    "softmax_fast_kernel")
+            op.run = lambda b: mbrt.softmax(b["x"], b["y"], 1.0)
+            ops.append(op)
+
+    # BL-4a rotary in place, bf16 q/k [480, 801, 64], f32 tables [801, 32]
+    cos_h, sin_h = mbrt.rotary_tables(801, 64, 10000.0)
+    cos, sin = torch.from_numpy(cos_h).to(dev), torch.from_numpy(sin_h).to(dev)
+    op = Op("bl4a_rotary_bf16", 4 * 480 * 801 * 64 * 2 + 2 * 801 * 32 * 4,
+            lambda: dict(q=randn((480, 801, 64), bf16), k=randn((480, 801, 64), bf16)), "rotary_vec_kernel")
+    op.run = lambda b: mbrt.rotary_(b["q"], b["k"], cos, sin, mbrt.LAYOUT_BHND)
+    ops.append(op)
+
+    # BL-4b permutes [4, 801, 60, 384] <-> [4, 60, 801, 384] bf16
+    n_el = 4 * 801 * 60 * 384
+    op = Op("bl4b_permute_btf_to_bft_bf16", 2 * n_el * 2,
+            lambda: dict(x=randn((4, 801, 60, 384), bf16), y=torch.empty((4, 60, 801, 384), dtype=bf16, device=dev)),
+            "row_copy_kernel")
+    op.run = lambda b: mbrt.strided_copy(b["x"].permute(0, 2, 1, 3), b["y"])
+    ops.append(op)
+    op = Op("bl4b_permute_bft_to_btf_bf16", 2 * n_el * 2,
+            lambda: dict(x=randn((4, 60, 801, 384), bf16), y=torch.empty((4, 801, 60, 384), dtype=bf16, device=dev)),
+            "row_copy_kernel")
+    op.run = lambda b: mbrt.strided_copy(b["x"].permute(0, 2, 1, 3), b["y"])
+    ops.append(op)
+
+    # BL-5 band split / merge, batch 4, stereo, 60 mel bands
+    fi, off, ind, cnt = bands
+    Bb, F, T = 4, 2050, 801
+    J = fi.numel()
+    op = Op("bl5a_band_gather_f32", Bb * F * T * 2 * 4 + Bb * T * J * 2 * 4 + J * 4,
+            lambda: dict(s=randn((Bb, F, T, 2)), y=torch.empty((Bb, T, J * 2), device=dev)), "band_gather_kernel")
+    op.run = lambda b: mbrt.band_gather(b["s"], fi, b["y"])
+    ops.append(op)
+    op = Op("bl5b_band_mask_merge_f32",
+            Bb * T * J * 2 * 4 + Bb * F * T * 2 * 4 + Bb * 2 * (F // 2) * T * 2 * 4 + (off.numel() + J) * 4 + F * 4,
+            lambda: dict(s=randn((Bb, F, T, 2)), m=randn((Bb, T, J * 2), std=0.5),
+                         y=torch.empty((Bb * 2, F // 2, T, 2), device=dev)), "band_merge_kernel")
+    op.run = lambda b: mbrt.band_mask_merge(b["s"], [b["m"]], off, ind, cnt, b["y"], 2)
+    ops.append(op)
+    return ops
+
+
+def band_tables(torch, mbrt):
+    """60-band stereo layout (sr 44100, n_fft 2048) and its per-freq CSR, built on the
+    host by the library (as the reference's loader does) and uploaded once."""
+    fi, _ = mbrt.mel_band_layout(44100.0, 2048, 60, 2)
+    off, ind, cnt, _ = mbrt.band_csr(fi, 2050)
+    t = lambda a: torch.from_numpy(a).to("cuda")
+    return t(fi), t(off), t(ind), t(cnt)
+
+
+def read_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), if present."""
+    if not TRAFFIC_SUMMARY.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_SUMMARY.read_text(), flags=re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(threads: int | None):
+    """Oracle float pipeline on a row sample of each op (OpenMP over rows)."""
+    import numpy as np
+
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle as O
+
+    if not O.LIB.exists():
+        O.build()
+    nthreads = threads or min(16, os.cpu_count() or 1)
+    O.set_threads(nthreads)
+    rng = np.random.default_rng(0x4D42520000)
+    frac = 16  # 1/16 of the rows of every op
+    rnd = lambda shape, std=1.0: (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+    bf = O.f32_to_bf16
+    jobs = []
+    R, D = 48060 // frac, 384
+    x, r, gm = rnd((R, D)), rnd((R, D)), rnd(D) * np.float32(0.02) + np.float32(1.0)
+    jobs.append(("bl1", 4 * R * D * 4, lambda: O.rms_norm(x, O.F32, gm, O.F32, O.F32, math.sqrt(D), 1e-8, res=r,
+                                                         sdt=O.F32, mode=O.FAST, want_sum=True)))
+    h = bf(rnd((48060 // frac, 1536), 1.5))
+    jobs.append(("bl2a", 2 * h.size * 2, lambda: O.bias_act(h, O.BF16, None, O.F32, O.BF16, 1, mode=O.FAST)))
+    h2 = bf(rnd((48060 // frac, 3072), 1.5))
+    jobs.append(("bl2b", h2.size * 2 * 3 // 2, lambda: O.glu(h2, O.BF16, O.BF16, mode=O.FAST)))
+    at, gl = bf(rnd((60 // 4, 8, 801, 64))), bf(rnd((60 // 4, 801, 8), 2.0))
+    jobs.append(("bl2c", 2 * at.size * 2 + gl.size * 2,
+                 lambda: O.gate_merge(at, O.BF16, gl, O.BF16, O.BF16, 15, 8, 801, 64, mode=O.FAST)))
+    for rows, cols in ((480 * 801 // frac, 801), (6408 * 60 // frac, 60)):
+        s32 = rnd((rows, cols), 3.0)
+        s16 = bf(s32)
+        jobs.append((f"bl3_{cols}_f32", 2 * s32.size * 4, lambda s32=s32: O.softmax(s32, O.F32, O.F32, 1.0, O.FAST)))
+        jobs.append((f"bl3_{cols}_bf16", 2 * s16.size * 2, lambda s16=s16: O.softmax(s16, O.BF16, O.BF16, 1.0, O.FAST)))
+    q, k = bf(rnd((480 // frac, 801, 64))), bf(rnd((480 // frac, 801, 64)))
+    cs, sn = O.rotary_tables(801, 64)
+    jobs.append(("bl4a", 4 * q.size * 2, lambda: O.rotary(q, k, O.BF16, cs, sn, O.F32, 801, 1, mode=O.FAST)))
+    p = bf(rnd((4, 801, 60 // 4, 384)))
+    pv = p.reshape(-1)
+    shp, strd = (4, 60 // 4, 801, 384), (801 * 15 * 384, 384, 15 * 384, 1)
+    jobs.append(("bl4b", 2 * p.size * 2, lambda: O.strided_copy(pv, shp, strd)))
+    mb = O.mel_bands()
+    J = mb["freq_indices"].size
+    T = 801 // 4
+    st = rnd((4, 2050, T, 2))
+    jobs.append(("bl5a", st.size * 4 + 4 * T * J * 2 * 4, lambda: O.band_gather(st, mb["freq_indices"], O.F32, 4, 2050, T)))
+    mk = rnd((4, T, J, 2), 0.5)
+    cnt = mb["bands_per_freq"].astype(np.float32)
+    jobs.append(("bl5b", mk.size * 4 + 2 * st.size * 4,
+                 lambda: O.band_mask_merge(st, [mk], O.F32, mb["csr_offsets"], mb["csr_indices"], cnt, O.F32, O.F32, 4,
+                                           2050, T, 2, mode=O.FAST)))
+    tot_b, tot_t = 0, 0.0
+    per = {}
+    for name, nb, fn in jobs:
+        fn()  # warm
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        t = statistics.median(ts)
+        per[name] = round(nb / t / 1e9, 2)
+        tot_b += nb
+        tot_t += t
+    return {
+        "value": round(tot_b / tot_t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": nthreads,
+        "kind": "port",
+        "sample": f"1/{frac} of the rows (or frames) of every BL-1..BL-5 op, oracle float pipeline "
+                  f"(oracle/oracle.cpp, ORC_FAST, OpenMP), median of 3 after 1 warm run; "
+                  f"algorithmic bytes {tot_b / 1e9:.3f} GB in {tot_t:.3f} s",
+        "per_op_gbs": per,
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "the ops shard per row with no exchange, so run one process per GPU.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import mbrt
+
+    torch.cuda.set_device(0)
+    bands = band_tables(torch, mbrt)
+    ops = build_ops(torch, mbrt, bands)
+    for op in ops:
+        first = op.make()
+        ws = sum(t.numel() * t.element_size() for t in first.values())
+        nsets = 1 if ws >= MALL_DEFEAT_BYTES else max(2, math.ceil(MALL_DEFEAT_BYTES / ws) + 1)
+        op.sets = [first] + [op.make() for _ in range(nsets - 1)]
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+
+    def step(i, record):
+        evs = []
+        for op in ops:
+            b = op.sets[i % len(op.sets)]
+            if record:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                op.run(b)
+                e1.record(stream)
+                evs.append((op, e0, e1))
+            else:
+                op.run(b)
+        return evs
+
+    for i in range(args.warmup):
+        step(i, False)
+    torch.cuda.synchronize()
+    all_evs = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        all_evs += step(i, True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    for op, e0, e1 in all_evs:
+        op.times_ms.append(e0.elapsed_time(e1))
+
+    per_op = {}
+    tot_bytes = 0
+    tot_ms = 0.0
+    for op in ops:
+        ms = statistics.mean(op.times_ms)
+        gbs = op.bytes / (ms * 1e-3) / 1e9
+        per_op[op.name] = {"bytes": op.bytes, "ms": round(ms, 5), "median_ms": round(statistics.median(op.times_ms), 5),
+                           "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                           "buffer_sets": len(op.sets), "kernel": op.kernel}
+        tot_bytes += op.bytes
+        tot_ms += ms
+    dom = max(ops, key=lambda o: statistics.mean(o.times_ms))
+    dom_ms = statistics.mean(dom.times_ms)
+    achieved = dom.bytes / (dom_ms * 1e-3) / 1e9
+    value = tot_bytes / (tot_ms * 1e-3) / 1e9
+
+    # plain copy of known size, outside the timed region: calibrates FETCH_SIZE/WRITE_SIZE
+    cal = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    cal_out = torch.empty_like(cal)
+    mbrt.strided_copy(cal, cal_out)
+    torch.cuda.synchronize()
+    del cal, cal_out
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "mbr_chunk_tensor_ops: BL-1..BL-5 at full MelBandRoformer chunk shape "
+                        "(T=801 frames, 60 bands, D=384, batch 4 band split), one pass per step",
+            "ms_tensor_ops_per_step": round(tot_ms, 4),
+            "frac_hbm_peak_all_ops": round(value / HBM_PEAK_GBS, 4),
+            "storage_dtypes": "f32 and bf16 per op name; all arithmetic in f32",
+            "mall_defeat": f"each op cycles >= {MALL_DEFEAT_BYTES / 1e9:.1f} GB of buffer sets",
+            "per_op": per_op,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom.kernel,
+            "op": dom.name,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic() if dom.name == "bl3_softmax_time_f32" else None,
+            "algorithmic_bytes": dom.bytes,
+            "avg_ms": round(dom_ms, 5),
+        },
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_threads),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+"""Build the gfx950 libraries in-tree with hipcc (no cmake/ninja needed).
+
+Outputs (git-ignored, shipped with the source tree):
+  mbr-cuda-tile_amd/lib/libmbrt.so        C-ABI + HIP kernels (include/mbrt.h)
+  mbr-cuda-tile_amd/lib/libmbrt_tensor.so C++ Tensor / tensor_tile:: / mbr_tile:: layer
+
+Usage: python mbr-cuda-tile_amd/build.py [-j N] [-v]
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shlex
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+HOST = PKG / "host"
+BUILD = PKG / "_build"
+LIB = PKG / "lib"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# Packed-FP32 VALU forms are disabled for every HIP translation unit.
+COMMON = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+    f"-I{REPO / 'include'}",
+    f"-I{CSRC}",
+    f"-I{HOST}",
+]
+
+KERNEL_SOURCES = [
+    "abi_common.cpp",
+    "k_elementwise.hip",
+    "k_layout.hip",
+    "k_reduce.hip",
+    "k_norm.hip",
+    "k_act.hip",
+    "k_softmax.hip",
+    "k_rotary.hip",
+    "k_band.hip",
+    "host_tables.cpp",
+]
+
+TENSOR_SOURCES = [
+    "hip_context.cpp",
+    "tensor.cpp",
+    "tensor_tile.cpp",
+    "mbr_tile.cpp",
+]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(shlex.quote(c) for c in cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        line for line in res.stdout.splitlines()
+        if "packed-fp32-ops" not in line and "feature flag" not in line
+    )
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out)
+
+
+def _compile(src: Path, obj: Path, verbose: bool) -> Path:
+    lang = ["-x", "hip"] if src.suffix in (".hip", ".cpp") else []
+    _run([HIPCC, *COMMON, *lang, "-c", str(src), "-o", str(obj)], verbose)
+    return obj
+
+
+def _objects(srcdir: Path, names: list[str], tag: str, jobs: int, verbose: bool) -> list[Path]:
+    BUILD.mkdir(parents=True, exist_ok=True)
+    objs = []
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = []
+        for n in names:
+            src = srcdir / n
+            obj = BUILD / f"{tag}_{Path(n).stem}.o"
+            futs.append(ex.submit(_compile, src, obj, verbose))
+        for f in futs:
+            objs.append(f.result())
+    return objs
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> dict[str, Path]:
+    """Compile every source and link both libraries; returns their paths."""
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    LIB.mkdir(parents=True, exist_ok=True)
+    kobjs = _objects(CSRC, KERNEL_SOURCES, "k", jobs, verbose)
+    libmbrt = LIB / "libmbrt.so"
+    tmp = libmbrt.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, kobjs)], verbose)
+    os.replace(tmp, libmbrt)
+    out = {"libmbrt": libmbrt}
+    tsrc = [n for n in TENSOR_SOURCES if (HOST / n).exists()]
+    if tsrc:
+        tobjs = _objects(HOST, tsrc, "t", jobs, verbose)
+        libt = LIB / "libmbrt_tensor.so"
+        tmp = libt.with_suffix(".so.tmp")
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, tobjs),
+              f"-L{LIB}", "-lmbrt", "-Wl,-rpath,$ORIGIN"], verbose)
+        os.replace(tmp, libt)
+        out["libmbrt_tensor"] = libt
+    return out
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("-v", action="store_true")
+    a = ap.parse_args(argv)
+    paths = build(a.j, a.v)
+    for k, p in paths.items():
+        print(f"{k}: {p}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

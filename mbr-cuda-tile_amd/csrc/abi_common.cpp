@@ -1,0 +1,44 @@
+// Thread-local error state and generic entry points of the C-ABI.
+#include "abi_common.hpp"
+
+namespace mbrt {
+
+static thread_local std::string t_error;
+
+int set_error(int status, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    t_error.assign(buf);
+    return status;
+}
+
+void clear_error() { t_error.clear(); }
+
+int check_launch(const char* op) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return set_error(MBRT_E_HIP, "%s: kernel launch failed: %s", op, hipGetErrorString(e));
+    }
+    return MBRT_OK;
+}
+
+}  // namespace mbrt
+
+extern "C" {
+
+const char* mbrt_last_error(void) { return mbrt::t_error.c_str(); }
+
+int mbrt_version(void) { return 1 * 10000 + 0 * 100 + 0; }
+
+int mbrt_stream_sync(mbrt_stream_t stream) {
+    hipError_t e = hipStreamSynchronize(mbrt::as_stream(stream));
+    if (e != hipSuccess) {
+        return mbrt::set_error(MBRT_E_HIP, "mbrt_stream_sync: %s", hipGetErrorString(e));
+    }
+    return MBRT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,274 @@
+// Mel band split / merge around the band-split transformer
+// (mbr_tile::gather_freqs_fold_complex and apply_mask_and_scatter,
+//  src/mbr_cuda_tile.cu:4554-4601, 5586-5803, 6215-6241, 7951-8081; zero_dc 5805-5838).
+//
+// Layouts (complex values are interleaved (re, im) f32 pairs, 8 bytes):
+//   stft  [B, F, T]      freq-major: F = bins * channels, freq = bin * channels + ch
+//   bands [B, T, J]      time-major: J band-bins, idx[j] = freq of band-bin j
+//   out   [B*S*C, bins, T]
+// Both directions are transposes between a freq-major and a time-major complex matrix,
+// so both stage 64-frame tiles through LDS: every global access is a run of consecutive
+// complex values along T (stft/out) or along J (bands), never a stride-T gather.
+//
+// Gather: a block owns (b, 64 frames, 64 band-bins).  It reads, for each band-bin j, the
+// 64 frames of stft row idx[j] (512 contiguous bytes), then writes, for each frame, the 64
+// band-bins (512 contiguous bytes of the output row).
+//
+// Merge: a block owns (b, stem, 32 freqs, 64 frames).  The band-bins that feed those
+// freqs are the CSR entries [off[f0], off[f0+32]) (<= 64 when no freq has more than 2
+// bands; larger lists are processed in chunks of 64).  Their mask rows are staged in LDS,
+// then each thread forms sum_e stft * mask_e over its freq's entries in ascending e and
+// divides by max(count, 1e-8).  Each output is written once: no float atomics and no
+// zero-fill pass, and the summation order is fixed.
+#include "abi_common.hpp"
+
+#include <algorithm>
+
+namespace mbrt {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTT = 64;   // frames per tile
+constexpr int kTJ = 64;   // band-bins per gather tile
+constexpr int kTF = 32;   // freqs per merge tile
+constexpr int kME = 64;   // CSR entries staged per merge chunk
+
+__device__ __forceinline__ int64_t load_index(const void* p, int i64, int64_t i) {
+    return i64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
+}
+
+struct GatherArgs {
+    const float* stft;
+    const void* idx;
+    int idx64;
+    void* out;
+    int odt;
+    int64_t F, T, J;
+};
+
+__global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
+    __shared__ f32x2 tile[kTJ][kTT + 1];
+    const int64_t j0 = (int64_t)blockIdx.x * kTJ;
+    const int64_t t0 = (int64_t)blockIdx.y * kTT;
+    const int64_t b = blockIdx.z;
+    const int lane = threadIdx.x % 64;
+    const int grp = threadIdx.x / 64;
+    const f32x2* stft = reinterpret_cast<const f32x2*>(a.stft) + b * a.F * a.T;
+    // read: row jj of the tile = stft[b, idx[j0+jj], t0 : t0+64]
+#pragma unroll 4
+    for (int jj = grp; jj < kTJ; jj += kThreads / 64) {
+        const int64_t j = j0 + jj, t = t0 + lane;
+        if (j < a.J && t < a.T) {
+            const int64_t f = load_index(a.idx, a.idx64, j);
+            tile[jj][lane] = stft[f * a.T + t];
+        }
+    }
+    __syncthreads();
+    // write: out[b, t0+tt, j0 : j0+64]
+#pragma unroll 4
+    for (int tt = grp; tt < kTT; tt += kThreads / 64) {
+        const int64_t j = j0 + lane, t = t0 + tt;
+        if (j < a.J && t < a.T) {
+            const f32x2 v = tile[lane][tt];
+            const int64_t o = (b * a.T + t) * a.J + j;
+            if (a.odt == F32) {
+                reinterpret_cast<f32x2*>(a.out)[o] = v;
+            } else if (a.odt == BF16) {
+                reinterpret_cast<uint32_t*>(a.out)[o] = pack_bf16x2(v.x, v.y);
+            } else {
+                reinterpret_cast<uint32_t*>(a.out)[o] = pack_f16x2(v.x, v.y);
+            }
+        }
+    }
+}
+
+struct MergeArgs {
+    const float* stft;
+    const void* mask[2];
+    int mdt;
+    int S;
+    const void* off;
+    const void* ind;
+    int idx64;
+    const void* cnt;
+    int cdt;
+    void* out;
+    int odt;
+    int64_t F, T, J, C;
+};
+
+__device__ __forceinline__ f32x2 load_mask(const void* p, int mdt, int64_t i) {
+    if (mdt == F32) return reinterpret_cast<const f32x2*>(p)[i];
+    const uint32_t w = reinterpret_cast<const uint32_t*>(p)[i];
+    if (mdt == BF16) return f32x2{bf16_lo(w), bf16_hi(w)};
+    return unpack_f16x2(w);
+}
+
+__global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
+    __shared__ f32x2 ms[kME][kTT + 1];
+    const int64_t t0 = (int64_t)blockIdx.x * kTT;
+    const int64_t f0 = (int64_t)blockIdx.y * kTF;
+    const int64_t bs = blockIdx.z;  // b * S + s
+    const int64_t b = bs / a.S, s = bs - b * a.S;
+    const void* mask = a.mask[s];
+    const int lane = threadIdx.x % 64;
+    const int grp = threadIdx.x / 64;
+    constexpr int kPer = kTF / (kThreads / 64);  // freqs per thread (8)
+    const int64_t t = t0 + lane;
+    const bool t_ok = t < a.T;
+
+    const int64_t f_end = f0 + kTF < a.F ? f0 + kTF : a.F;
+    const int64_t e_begin = load_index(a.off, a.idx64, f0);
+    const int64_t e_end = load_index(a.off, a.idx64, f_end);
+
+    // this thread's freqs: f0 + grp + 4*r
+    f32x2 sv[kPer], acc[kPer];
+    int64_t eb[kPer], ee[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int64_t f = f0 + grp + 4 * r;
+        acc[r] = f32x2{0.0f, 0.0f};
+        eb[r] = ee[r] = 0;
+        sv[r] = f32x2{0.0f, 0.0f};
+        if (f < a.F) {
+            eb[r] = load_index(a.off, a.idx64, f);
+            ee[r] = load_index(a.off, a.idx64, f + 1);
+            if (t_ok) sv[r] = reinterpret_cast<const f32x2*>(a.stft)[(b * a.F + f) * a.T + t];
+        }
+    }
+    const f32x2* mrow = nullptr;
+    (void)mrow;
+    for (int64_t c0 = e_begin; c0 < e_end; c0 += kME) {
+        const int64_t c1 = c0 + kME < e_end ? c0 + kME : e_end;
+        // stage mask[b, t0 : t0+64, indices[c0 : c1]] as ms[e - c0][tt]
+        for (int tt = grp; tt < kTT; tt += kThreads / 64) {
+            const int64_t e = c0 + lane, tq = t0 + tt;
+            if (e < c1 && tq < a.T) {
+                const int64_t j = load_index(a.ind, a.idx64, e);
+                ms[lane][tt] = load_mask(mask, a.mdt, (b * a.T + tq) * a.J + j);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int64_t lo = eb[r] > c0 ? eb[r] : c0;
+            const int64_t hi = ee[r] < c1 ? ee[r] : c1;
+            for (int64_t e = lo; e < hi; ++e) {
+                const f32x2 m = ms[e - c0][lane];
+                acc[r].x += sv[r].x * m.x - sv[r].y * m.y;
+                acc[r].y += sv[r].x * m.y + sv[r].y * m.x;
+            }
+        }
+        __syncthreads();
+    }
+    if (!t_ok) return;
+#pragma unroll
+    for (int r = 0; r < kPer; ++r) {
+        const int64_t f = f0 + grp + 4 * r;
+        if (f >= a.F) continue;
+        float den = load1(a.cnt, a.cdt, f);
+        den = den > 1.0e-8f ? den : 1.0e-8f;
+        const float inv = 1.0f / den;
+        const int64_t bin = f / a.C, ch = f - bin * a.C;
+        const int64_t bins = a.F / a.C;
+        const int64_t o = (((b * a.S + s) * a.C + ch) * bins + bin) * a.T + t;
+        const float re = acc[r].x * inv, im = acc[r].y * inv;
+        if (a.odt == F32) {
+            reinterpret_cast<f32x2*>(a.out)[o] = f32x2{re, im};
+        } else if (a.odt == BF16) {
+            reinterpret_cast<uint32_t*>(a.out)[o] = pack_bf16x2(re, im);
+        } else {
+            reinterpret_cast<uint32_t*>(a.out)[o] = pack_f16x2(re, im);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void zero_dc_kernel(void* spec, int dt, int64_t outer, int64_t bins, int64_t T) {
+    const int64_t per = T * 2;
+    const int64_t n = outer * per;
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i < n; i += (int64_t)gridDim.x * kThreads) {
+        const int64_t o = i / per, r = i - o * per;
+        const int64_t e = o * bins * per + r;
+        if (dt == F32) reinterpret_cast<float*>(spec)[e] = 0.0f;
+        else reinterpret_cast<uint16_t*>(spec)[e] = 0;
+    }
+}
+
+}  // namespace
+}  // namespace mbrt
+
+using namespace mbrt;
+
+extern "C" {
+
+int mbrt_band_gather(const float* stft, const void* freq_indices, int index_dtype, void* out, int out_dtype, int64_t B,
+                     int64_t total_freq, int64_t frames, int64_t n_band_freqs, mbrt_stream_t stream) {
+    const char* op = "mbrt_band_gather";
+    MBRT_REQUIRE(is_index_dt(index_dtype), MBRT_E_UNSUPPORTED_DTYPE, "%s: indices must be I32/I64", op);
+    MBRT_REQUIRE_FLOAT_DT(out_dtype, op);
+    MBRT_REQUIRE(B >= 0 && total_freq >= 1 && frames >= 0 && n_band_freqs >= 0, MBRT_E_SHAPE, "%s: bad shape", op);
+    if (B == 0 || frames == 0 || n_band_freqs == 0) return MBRT_OK;
+    MBRT_REQUIRE(stft && freq_indices && out, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
+    MBRT_REQUIRE(aligned(stft, 8) && aligned(out, out_dtype == F32 ? 8 : 4), MBRT_E_ALIGN,
+                 "%s: complex buffers must be aligned to one complex value", op);
+    MBRT_REQUIRE(B <= 65535, MBRT_E_SHAPE, "%s: batch %lld exceeds 65535", op, (long long)B);
+    GatherArgs a{stft, freq_indices, index_dtype == I64, out, out_dtype, total_freq, frames, n_band_freqs};
+    const dim3 grid((unsigned)ceil_div(n_band_freqs, kTJ), (unsigned)ceil_div(frames, kTT), (unsigned)B);
+    hipLaunchKernelGGL(band_gather_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+    return check_launch(op);
+}
+
+int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_dtype, int num_stems,
+                         const void* csr_offsets, const void* csr_indices, int index_dtype, const void* counts,
+                         int counts_dtype, void* out, int out_dtype, int64_t B, int64_t total_freq, int64_t frames,
+                         int64_t n_band_freqs, int64_t channels, mbrt_stream_t stream) {
+    const char* op = "mbrt_band_mask_merge";
+    MBRT_REQUIRE(num_stems == 1 || num_stems == 2, MBRT_E_INVALID_ARG, "%s: expected one or two stems", op);
+    MBRT_REQUIRE(is_index_dt(index_dtype), MBRT_E_UNSUPPORTED_DTYPE, "%s: CSR must be I32/I64", op);
+    MBRT_REQUIRE_FLOAT_DT(mask_dtype, op);
+    MBRT_REQUIRE(counts_dtype == F32 || counts_dtype == BF16, MBRT_E_UNSUPPORTED_DTYPE, "%s: counts must be F32/BF16", op);
+    MBRT_REQUIRE_FLOAT_DT(out_dtype, op);
+    MBRT_REQUIRE(channels >= 1 && total_freq >= 1 && total_freq % channels == 0, MBRT_E_SHAPE,
+                 "%s: invalid audio channel count", op);
+    MBRT_REQUIRE(B >= 0 && frames >= 0 && n_band_freqs >= 0, MBRT_E_SHAPE, "%s: bad shape", op);
+    if (B == 0 || frames == 0) return MBRT_OK;
+    MBRT_REQUIRE(stft && masks && csr_offsets && counts && out && (n_band_freqs == 0 || csr_indices),
+                 MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
+    for (int s = 0; s < num_stems; ++s) MBRT_REQUIRE(masks[s] != nullptr, MBRT_E_INVALID_ARG, "%s: NULL mask", op);
+    MBRT_REQUIRE(B * num_stems <= 65535, MBRT_E_SHAPE, "%s: batch*stems exceeds 65535", op);
+    MergeArgs a{};
+    a.stft = stft;
+    a.mask[0] = masks[0];
+    a.mask[1] = num_stems == 2 ? masks[1] : masks[0];
+    a.mdt = mask_dtype;
+    a.S = num_stems;
+    a.off = csr_offsets;
+    a.ind = csr_indices;
+    a.idx64 = index_dtype == I64;
+    a.cnt = counts;
+    a.cdt = counts_dtype;
+    a.out = out;
+    a.odt = out_dtype;
+    a.F = total_freq;
+    a.T = frames;
+    a.J = n_band_freqs;
+    a.C = channels;
+    const dim3 grid((unsigned)ceil_div(frames, kTT), (unsigned)ceil_div(total_freq, kTF), (unsigned)(B * num_stems));
+    hipLaunchKernelGGL(band_merge_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+    return check_launch(op);
+}
+
+int mbrt_zero_dc(void* spec, int dtype, int64_t outer, int64_t freq_bins, int64_t frames, mbrt_stream_t stream) {
+    const char* op = "mbrt_zero_dc";
+    MBRT_REQUIRE_FLOAT_DT(dtype, op);
+    MBRT_REQUIRE(outer >= 0 && freq_bins >= 1 && frames >= 0, MBRT_E_SHAPE, "%s: bad shape", op);
+    const int64_t n = outer * frames * 2;
+    if (n == 0) return MBRT_OK;
+    MBRT_REQUIRE(spec != nullptr, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
+    hipLaunchKernelGGL(zero_dc_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, kThreads), 1 << 20)), dim3(kThreads),
+                       0, as_stream(stream), spec, dtype, outer, freq_bins, frames);
+    return check_launch(op);
+}
+
+}  // extern "C"

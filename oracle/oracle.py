@@ -1,0 +1,298 @@
+"""numpy wrapper of liboracle.so — TEST INFRASTRUCTURE ONLY (the checker of the GPU
+kernels; see oracle.h).  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg import it.
+
+Storage conventions: f32 -> np.float32; bf16 and f16 -> np.uint16 bit patterns;
+indices -> np.int32 / np.int64.  Dtype codes match the C-ABI (F32=0, F16=1, I64=2,
+BF16=3, I32=4).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+
+F32, F16, I64, BF16, I32 = 0, 1, 2, 3, 4
+EXACT, FAST = 0, 1
+
+_NP = {F32: np.float32, F16: np.uint16, BF16: np.uint16, I64: np.int64, I32: np.int32}
+
+_lib: C.CDLL | None = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            raise ImportError(f"oracle: {LIB} is not built (make -C oracle)")
+        _lib = C.CDLL(str(LIB))
+        _lib.orc_mel_bands.restype = C.c_int64
+        _lib.orc_get_threads.restype = C.c_int
+    return _lib
+
+
+def _p(a):
+    if a is None:
+        return C.c_void_p(0)
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _i64arr(xs):
+    return (C.c_int64 * max(len(xs), 1))(*xs)
+
+
+L = C.c_int64
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def empty(shape, dt) -> np.ndarray:
+    return np.empty(shape, dtype=_NP[dt])
+
+
+# ---- inputs / conversions ---------------------------------------------------------------
+
+def randn(shape, seed: int, stream: int = 0, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    lib().orc_randn(_p(out), L(out.size), C.c_uint64(seed), C.c_uint64(stream), C.c_double(mean), C.c_double(std))
+    return out
+
+
+def randu64(n: int, seed: int, stream: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint64)
+    lib().orc_randu64(_p(out), L(n), C.c_uint64(seed), C.c_uint64(stream))
+    return out
+
+
+def f32_to_bf16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().orc_f32_to_bf16(_p(a), _p(out), L(a.size))
+    return out
+
+
+def bf16_to_f32(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().orc_bf16_to_f32(_p(a), _p(out), L(a.size))
+    return out
+
+
+def f32_to_f16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16(_p(a), _p(out), L(a.size))
+    return out
+
+
+def f16_to_f32(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().orc_f16_to_f32(_p(a), _p(out), L(a.size))
+    return out
+
+
+def f64_to_bf16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().orc_f64_to_bf16(_p(a), _p(out), L(a.size))
+    return out
+
+
+def to_f32(a: np.ndarray, dt: int) -> np.ndarray:
+    if dt == F32:
+        return np.asarray(a, dtype=np.float32)
+    if dt == BF16:
+        return bf16_to_f32(a)
+    if dt == F16:
+        return f16_to_f32(a)
+    return np.asarray(a, dtype=np.float32)
+
+
+def from_f32(a: np.ndarray, dt: int) -> np.ndarray:
+    if dt == F32:
+        return np.ascontiguousarray(a, dtype=np.float32)
+    if dt == BF16:
+        return f32_to_bf16(a)
+    if dt == F16:
+        return f32_to_f16(a)
+    raise ValueError(dt)
+
+
+def convert(src: np.ndarray, sdt: int, ddt: int) -> np.ndarray:
+    out = empty(src.shape, ddt)
+    lib().orc_convert(_p(src), sdt, _p(out), ddt, L(src.size))
+    return out
+
+
+# ---- tensor library -----------------------------------------------------------------------
+
+def binary(a, b, dt, op):
+    out = empty(a.shape, dt)
+    lib().orc_binary(_p(a), _p(b), _p(out), dt, L(a.size), op)
+    return out
+
+
+def binary_broadcast(a, b, dt, out_shape, a_strides, b_strides, op):
+    out = empty(out_shape, dt)
+    nd = len(out_shape)
+    lib().orc_binary_broadcast(_p(a), _p(b), _p(out), dt, nd, _i64arr(out_shape), _i64arr(a_strides),
+                               _i64arr(b_strides), op)
+    return out
+
+
+def strided_copy(src: np.ndarray, shape, strides) -> np.ndarray:
+    """src: flat contiguous storage; returns the contiguous tensor of the strided view."""
+    out = np.empty(shape, dtype=src.dtype)
+    lib().orc_strided_copy(_p(src), _p(out), src.itemsize, len(shape), _i64arr(shape), _i64arr(strides))
+    return out
+
+
+def index_select(src: np.ndarray, out_shape, strides, sel: int, idx: np.ndarray) -> np.ndarray:
+    idx = np.ascontiguousarray(idx, dtype=np.int64)
+    out = np.empty(out_shape, dtype=src.dtype)
+    lib().orc_index_select(_p(src), _p(out), src.itemsize, len(out_shape), _i64arr(out_shape), _i64arr(strides), sel,
+                           _p(idx))
+    return out
+
+
+def pad(src, dt, dst_shape, before, value=0.0, reflect=False):
+    out = empty(dst_shape, dt)
+    lib().orc_pad(_p(src), _p(out), dt, src.ndim, _i64arr(src.shape), _i64arr(dst_shape), _i64arr(before),
+                  C.c_float(value), 1 if reflect else 0)
+    return out
+
+
+def reduce_last(src, op, mode=EXACT):
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    inner = src.shape[-1]
+    out = np.empty(src.shape[:-1], dtype=np.float32)
+    lib().orc_reduce_last(_p(src), _p(out), L(src.size // max(inner, 1)), L(inner), op, mode)
+    return out
+
+
+def reduce_general(src, dim, op):
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    dim = dim % src.ndim
+    outer = int(np.prod(src.shape[:dim], dtype=np.int64))
+    inner = int(np.prod(src.shape[dim + 1:], dtype=np.int64))
+    out = np.empty(src.shape[:dim] + src.shape[dim + 1:], dtype=np.float32)
+    lib().orc_reduce_general(_p(src), _p(out), L(outer), L(src.shape[dim]), L(inner), op)
+    return out
+
+
+# ---- hot-path ops -------------------------------------------------------------------------
+
+def rms_norm(x, xdt, gamma, gdt, odt, scale, eps, res=None, sdt=F32, mode=EXACT, want_sum=False):
+    dim = x.shape[-1]
+    rows = x.size // dim
+    out = empty(x.shape, odt)
+    sum_out = empty(x.shape, sdt) if (res is not None and want_sum) else None
+    lib().orc_rms_norm(_p(x), xdt, _p(res), _p(gamma), gdt, _p(sum_out), sdt, _p(out), odt, L(rows), L(dim),
+                       C.c_float(scale), C.c_float(eps), mode)
+    return (out, sum_out) if want_sum else out
+
+
+def bias_act(x, xdt, bias, bdt, odt, act, mode=EXACT):
+    cols = x.shape[-1]
+    out = empty(x.shape, odt)
+    lib().orc_bias_act(_p(x), xdt, _p(bias), bdt, _p(out), odt, L(x.size // cols), L(cols), act, mode)
+    return out
+
+
+def glu(x, xdt, odt, mode=EXACT):
+    full = x.shape[-1]
+    out = empty(x.shape[:-1] + (full // 2,), odt)
+    lib().orc_glu(_p(x), xdt, _p(out), odt, L(x.size // full), L(full // 2), mode)
+    return out
+
+
+def gate_merge(attn, adt, gate, gdt, odt, B, H, N, D, layout=0, logit=True, mode=EXACT):
+    out = empty((B, N, H * D), odt)
+    lib().orc_gate_merge(_p(attn), adt, _p(gate), gdt, 1 if logit else 0, _p(out), odt, L(B), L(H), L(N), L(D),
+                         layout, mode)
+    return out
+
+
+def softmax(x, idt, odt, scale=1.0, mode=EXACT):
+    cols = x.shape[-1]
+    out = empty(x.shape, odt)
+    lib().orc_softmax(_p(x), idt, _p(out), odt, L(x.size // cols), L(cols), C.c_float(scale), mode)
+    return out
+
+
+def rotary_tables(seq: int, dim_head: int, theta: float = 10000.0):
+    cos = np.empty((seq, dim_head // 2), dtype=np.float32)
+    sin = np.empty((seq, dim_head // 2), dtype=np.float32)
+    lib().orc_rotary_tables(_p(cos), _p(sin), L(seq), L(dim_head), C.c_float(theta))
+    return cos, sin
+
+
+def rotary(q, k, dt, cos, sin, tdt, n_pos, heads, layout=0, mode=EXACT):
+    """Returns rotated copies of q (and k)."""
+    q = q.copy()
+    k = k.copy() if k is not None else None
+    D = q.shape[-1]
+    lib().orc_rotary(_p(q), _p(k), dt, _p(cos), _p(sin), tdt, L(q.size // D), L(n_pos), L(heads), L(D), layout, mode)
+    return q, k
+
+
+def split_qkv(qkv, idt, cos, sin, tdt, odt, B, N, H, D, out_n, mode=EXACT):
+    q = empty((B, H, out_n, D), odt)
+    k = empty((B, H, out_n, D), odt)
+    v = empty((B, H, out_n, D), odt)
+    lib().orc_split_qkv(_p(qkv), idt, _p(cos), _p(sin), tdt, _p(q), _p(k), _p(v), odt, L(B), L(N), L(H), L(D),
+                        L(out_n), mode)
+    return q, k, v
+
+
+def mel_bands(sr=44100.0, n_fft=2048, n_bands=60, channels=2):
+    """Returns dict(freq_indices, freqs_per_band, bands_per_freq, csr_offsets, csr_indices) (int32)."""
+    J = lib().orc_mel_bands(C.c_double(sr), n_fft, n_bands, channels, None, None, None, None, None)
+    F = (n_fft // 2 + 1) * channels
+    fi = np.empty(J, dtype=np.int32)
+    fpb = np.empty(n_bands, dtype=np.int32)
+    bpf = np.empty(F, dtype=np.int32)
+    off = np.empty(F + 1, dtype=np.int32)
+    ind = np.empty(J, dtype=np.int32)
+    lib().orc_mel_bands(C.c_double(sr), n_fft, n_bands, channels, _p(fi), _p(fpb), _p(bpf), _p(off), _p(ind))
+    return dict(freq_indices=fi, freqs_per_band=fpb, bands_per_freq=bpf, csr_offsets=off, csr_indices=ind)
+
+
+def band_gather(stft, idx, odt, B, F, T):
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    J = idx.size
+    out = empty((B, T, J * 2), odt)
+    lib().orc_band_gather(_p(stft), _p(idx), _p(out), odt, L(B), L(F), L(T), L(J))
+    return out
+
+
+def band_mask_merge(stft, masks, mdt, off, ind, cnt, cdt, odt, B, F, T, C_ch, mode=EXACT):
+    off = np.ascontiguousarray(off, dtype=np.int32)
+    ind = np.ascontiguousarray(ind, dtype=np.int32)
+    S = len(masks)
+    J = ind.size
+    out = empty((B * S * C_ch, F // C_ch, T, 2), odt)
+    arr = (C.c_void_p * S)(*[m.ctypes.data for m in masks])
+    lib().orc_band_mask_merge(_p(stft), arr, mdt, S, _p(off), _p(ind), _p(cnt), cdt, _p(out), odt, L(B), L(F), L(T),
+                              L(J), L(C_ch), mode)
+    return out
+
+
+def zero_dc(spec, dt):
+    spec = spec.copy()
+    outer, bins, T, _ = spec.shape
+    lib().orc_zero_dc(_p(spec), dt, L(outer), L(bins), L(T))
+    return spec

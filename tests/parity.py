@@ -1,0 +1,107 @@
+"""Parity rules shared by the tests.
+
+* Integer / byte / index work and pure copies: bit-exact.
+* f32 outputs: max_i |y_i - yhat_i| / max(|yhat_i|, tau) <= 1e-5, tau = 1e-3 * RMS(yhat),
+  where yhat is the oracle's double-precision value rounded once to f32.
+* bf16 / f16 outputs: one correct rounding alone can move a value by 2^-8 (bf16), which
+  exceeds 2e-3, so the rule compares against yhat = the double-precision value rounded
+  once to the output format: |y_i - yhat_i| <= 1 ulp(max(|yhat_i|, tau)) elementwise,
+  and ||y - yhat||_2 / ||yhat||_2 <= 2e-3 norm-wise.
+NaN positions must agree; infinities must agree exactly.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32, F16, I64, BF16, I32 = 0, 1, 2, 3, 4
+
+RTOL_F32 = 1e-5
+NORM_RTOL_LOWP = 2e-3
+TAU_REL = 1e-3
+
+
+def _f32(a: np.ndarray, dt: int) -> np.ndarray:
+    if dt == F32:
+        return np.asarray(a, dtype=np.float32).astype(np.float64)
+    if dt == BF16:
+        return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    if dt == F16:
+        return np.asarray(a, dtype=np.uint16).view(np.float16).astype(np.float64)
+    raise ValueError(dt)
+
+
+def _check_specials(y: np.ndarray, yh: np.ndarray, what: str) -> np.ndarray:
+    ny, nh = np.isnan(y), np.isnan(yh)
+    assert np.array_equal(ny, nh), f"{what}: NaN positions differ ({int((ny != nh).sum())} elements)"
+    iy, ih = np.isinf(y), np.isinf(yh)
+    assert np.array_equal(iy, ih) and np.array_equal(y[iy], yh[ih]), f"{what}: infinities differ"
+    return ~(ny | iy)
+
+
+def assert_bitexact(y: np.ndarray, yhat: np.ndarray, what: str = "") -> None:
+    y = np.ascontiguousarray(y)
+    yhat = np.ascontiguousarray(yhat)
+    assert y.shape == yhat.shape, f"{what}: shape {y.shape} != {yhat.shape}"
+    assert y.dtype.itemsize == yhat.dtype.itemsize, f"{what}: element sizes differ"
+    if y.size == 0:
+        return
+    fy, fh = y.reshape(-1), yhat.reshape(-1)
+    by, bh = fy.view(np.uint8).reshape(fy.size, -1), fh.view(np.uint8).reshape(fh.size, -1)
+    diff = np.nonzero((by != bh).any(axis=1))[0]
+    if diff.size:
+        raise AssertionError(f"{what}: {diff.size} of {fy.size} elements differ; first at {diff[:5]}: "
+                             f"{fy[diff[:5]]} vs {fh[diff[:5]]}")
+
+
+def rel_errors(y: np.ndarray, yhat: np.ndarray, dt: int) -> tuple[float, float]:
+    """(max elementwise error relative to max(|yhat|, tau), norm-wise relative error)."""
+    a, b = _f32(y, dt).reshape(-1), _f32(yhat, dt).reshape(-1)
+    ok = np.isfinite(a) & np.isfinite(b)
+    a, b = a[ok], b[ok]
+    if b.size == 0:
+        return 0.0, 0.0
+    tau = TAU_REL * float(np.sqrt(np.mean(b * b)))
+    den = np.maximum(np.abs(b), tau if tau > 0 else 1e-30)
+    elem = float(np.max(np.abs(a - b) / den))
+    nb = float(np.linalg.norm(b))
+    norm = float(np.linalg.norm(a - b) / nb) if nb > 0 else float(np.linalg.norm(a - b))
+    return elem, norm
+
+
+def _ulp(x: np.ndarray, dt: int) -> np.ndarray:
+    p, emin = (8, -126) if dt == BF16 else (11, -14)
+    ax = np.maximum(np.abs(x), np.finfo(np.float64).tiny)
+    e = np.floor(np.log2(ax))
+    e = np.maximum(e, emin)
+    return np.exp2(e - (p - 1))
+
+
+def assert_close(y: np.ndarray, yhat: np.ndarray, dt: int, what: str = "", rtol: float | None = None) -> dict:
+    """Apply the rule for output dtype `dt` (F32 / BF16 / F16); returns the measured errors."""
+    assert y.shape == yhat.shape, f"{what}: shape {y.shape} != {yhat.shape}"
+    a, b = _f32(y, dt), _f32(yhat, dt)
+    ok = _check_specials(a, b, what)
+    a, b = a[ok], b[ok]
+    if b.size == 0:
+        return {"max_rel": 0.0, "norm_rel": 0.0}
+    tau = TAU_REL * float(np.sqrt(np.mean(b * b)))
+    if dt == F32:
+        tol = RTOL_F32 if rtol is None else rtol
+        den = np.maximum(np.abs(b), tau if tau > 0 else 1e-30)
+        err = np.abs(a - b) / den
+        worst = int(np.argmax(err))
+        assert err[worst] <= tol, (f"{what}: f32 max rel err {err[worst]:.3e} > {tol:.0e} at {worst}: "
+                                   f"got {a[worst]!r} want {b[worst]!r}")
+        elem = float(err[worst])
+    else:
+        ulp = _ulp(np.maximum(np.abs(b), tau), dt)
+        err = np.abs(a - b) / ulp
+        worst = int(np.argmax(err))
+        assert err[worst] <= 1.0 + 1e-9, (f"{what}: {err[worst]:.2f} ulp off at {worst}: got {a[worst]!r} "
+                                          f"want {b[worst]!r}")
+        elem = float(np.max(np.abs(a - b) / np.maximum(np.abs(b), tau if tau > 0 else 1e-30)))
+    nb = float(np.linalg.norm(b))
+    norm = float(np.linalg.norm(a - b) / nb) if nb > 0 else float(np.linalg.norm(a - b))
+    if dt != F32:
+        assert norm <= NORM_RTOL_LOWP, f"{what}: norm-wise rel err {norm:.3e} > {NORM_RTOL_LOWP}"
+    return {"max_rel": elem, "norm_rel": norm}

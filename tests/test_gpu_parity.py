@@ -1,0 +1,535 @@
+"""GPU parity of every C-ABI entry point against the CPU oracle.
+
+Inputs are seeded (oracle RNG) and copied to the device; outputs come back through the
+C-ABI (mbrt ctypes binding) and are compared with the oracle on the same inputs under
+the rules in parity.py: bit-exact for copies, gathers and integer work; 1e-5 relative
+(f32) or 1 ulp + 2e-3 norm-wise (bf16/f16) for float math.  The BASELINE shapes run at
+full size where the oracle finishes in seconds, otherwise on a sampled set of rows plus
+size-independent properties over the whole tensor.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import mbrt
+import oracle as O
+from gpu_util import empty, say, to_dev, to_host
+from parity import BF16, F16, F32, I32, I64, assert_bitexact, assert_close
+
+pytestmark = pytest.mark.gpu
+
+SEED = {1: 0x4D42520001, 2: 0x4D42520002, 3: 0x4D42520003, 4: 0x4D42520004, 5: 0x4D42520005}
+
+
+def inp(orc, shape, seed, stream, dt=F32, mean=0.0, std=1.0):
+    x = orc.randn(shape, seed=seed, stream=stream, mean=mean, std=std)
+    return x if dt == F32 else orc.from_f32(x, dt)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _threads(orc):
+    orc.set_threads(8)
+
+
+# ---- layout ---------------------------------------------------------------------------------
+
+def test_permute_btfd_bftd_full_bitexact(orc, dev):
+    say("permute bf16 [4,801,60,384] <-> [4,60,801,384]")
+    x = inp(orc, (4, 801, 60, 384), SEED[4], 1, BF16)
+    xd = to_dev(x, BF16)
+    y = empty((4, 60, 801, 384), BF16)
+    mbrt.strided_copy(xd.permute(0, 2, 1, 3), y)
+    back = empty((4, 801, 60, 384), BF16)
+    mbrt.strided_copy(y.permute(0, 2, 1, 3), back)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(y, BF16), np.ascontiguousarray(x.transpose(0, 2, 1, 3)), "permute")
+    assert_bitexact(to_host(back, BF16), x, "permute round trip")
+
+
+@pytest.mark.parametrize("dt", [F32, BF16, I64, I32, F16])
+@pytest.mark.parametrize("perm,shape", [
+    ((0, 2, 1, 3), (3, 17, 5, 24)),       # inner dim kept: row copies
+    ((0, 2, 1, 3), (2, 9, 7, 3)),         # odd runs: narrow vectors
+    ((1, 0), (67, 130)),                  # true transpose: LDS tiles
+    ((0, 2, 1), (3, 70, 129)),            # batched transpose
+    ((2, 1, 0), (5, 3, 4)),               # small: element path
+    ((0, 2, 1, 3, 4), (2, 2, 9, 11, 2)),  # stft [B,S,F,T,2] -> [B,F,S,T,2]
+])
+def test_strided_copy_generic(orc, dev, dt, perm, shape):
+    say(f"strided_copy dt={dt} perm={perm} shape={shape}")
+    rng = np.random.default_rng(hash((dt, perm, shape)) % 2**32)
+    npdt = {F32: np.float32, BF16: np.uint16, F16: np.uint16, I64: np.int64, I32: np.int32}[dt]
+    x = rng.integers(0, 2**15, size=shape).astype(npdt)
+    xd = to_dev(x, dt)
+    v = xd.permute(*perm)
+    y = empty(v.shape, dt)
+    mbrt.strided_copy(v, y)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(y, dt), np.ascontiguousarray(x.transpose(perm)), "strided copy")
+
+
+def test_strided_copy_sliced_views(orc, dev):
+    say("strided_copy of sliced, offset views")
+    x = orc.randn((8, 33, 20), seed=5)
+    xd = to_dev(x, F32)
+    for v, ref in [(xd[:, 1:30, 3:17], x[:, 1:30, 3:17]), (xd[2:7, :, 1:], x[2:7, :, 1:]),
+                   (xd[:, ::2, :], x[:, ::2, :]), (xd.permute(2, 0, 1)[5:9], x.transpose(2, 0, 1)[5:9])]:
+        y = empty(v.shape, F32)
+        mbrt.strided_copy(v, y)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(y, F32), np.ascontiguousarray(ref), "sliced view")
+
+
+def test_index_select_pad_cat(orc, dev):
+    say("index_select / pad / cat")
+    x = orc.randn((6, 50, 8), seed=6)
+    xd = to_dev(x, F32)
+    for idt in (I64, I32):
+        idx = np.array([3, 0, 49, 7, 7, 12], dtype=np.int64 if idt == I64 else np.int32)
+        out = empty((6, 6, 8), F32)
+        mbrt.index_select(xd, 1, to_dev(idx, idt), out)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(out, F32), np.take(x, idx, axis=1), "index_select")
+    for reflect in (False, True):
+        out = empty((6, 50, 15), F32)
+        mbrt.pad(xd, out, [0, 0, 4], value=2.5, reflect=reflect)
+        torch.cuda.synchronize()
+        ref = np.pad(x, ((0, 0), (0, 0), (4, 3)), mode="reflect") if reflect else \
+            np.pad(x, ((0, 0), (0, 0), (4, 3)), constant_values=2.5)
+        assert_bitexact(to_host(out, F32), ref, f"pad reflect={reflect}")
+    parts = [orc.randn((4, n, 6), seed=60 + n) for n in (3, 1, 5)]
+    out = empty((4, 9, 6), F32)
+    mbrt.cat([to_dev(p, F32) for p in parts], 1, out)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(out, F32), np.concatenate(parts, axis=1), "cat")
+
+
+# ---- element-wise ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [0, 1, 7, 8, 1000, 4099])
+def test_fill_arange_convert(orc, dev, n):
+    say(f"fill/arange/convert n={n}")
+    for dt in (F32, BF16, F16, I64, I32):
+        t = empty((n,), dt)
+        mbrt.fill_(t, 3.25 if dt not in (I64, I32) else 7)
+        torch.cuda.synchronize()
+        want = {F32: 3.25, BF16: 3.25, F16: 3.25, I64: 7, I32: 7}[dt]
+        assert np.all(to_host(t, dt) == (orc.from_f32(np.full(n, want, np.float32), dt) if dt in (BF16, F16) else want))
+    for dt in (F32, I64, I32, F16):
+        t = empty((n,), dt)
+        mbrt.arange_(t, -3)
+        torch.cuda.synchronize()
+        ref = np.arange(-3, n - 3)
+        ref = orc.from_f32(ref.astype(np.float32), dt) if dt in (F32, F16) else ref.astype(t.cpu().numpy().dtype)
+        assert_bitexact(to_host(t, dt), ref, f"arange dt={dt}")
+    x = orc.randn(n, seed=7, std=100.0)
+    for sdt, ddt in [(F32, BF16), (BF16, F32), (F32, F16), (F16, F32), (BF16, F16), (F32, I64), (I64, F32),
+                     (F32, I32), (I32, BF16)]:
+        src = orc.convert(x, F32, sdt) if sdt != F32 else x
+        out = empty((n,), ddt)
+        mbrt.convert(to_dev(src, sdt), out)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(out, ddt), orc.convert(src, sdt, ddt), f"convert {sdt}->{ddt}")
+
+
+def test_convert_bf16_specials(orc, dev):
+    say("convert f32->bf16 special values and ties")
+    u = np.array([0x7f7fffff, 0x7f7f8000, 0x7f7f7fff, 0x3f808000, 0x3f818000, 0x00008000, 0x80018000, 0x7f800000,
+                  0xff800000, 0x00000001, 0x80000000, 0x3f800000], dtype=np.uint32)
+    rng = np.random.default_rng(8)
+    u = np.concatenate([u, (rng.integers(0, 2**16, 5000).astype(np.uint32) << 16) | 0x8000,
+                        rng.integers(0, 2**32, 20000, dtype=np.uint64).astype(np.uint32)])
+    f = u.view(np.float32)
+    f = f[~np.isnan(f)]
+    out = empty(f.shape, BF16)
+    mbrt.convert(to_dev(f, F32), out)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(out, BF16), orc.f32_to_bf16(f), "f32->bf16 RNE")
+    nan = np.array([np.nan, -np.nan], np.float32)
+    out = empty((2,), BF16)
+    mbrt.convert(to_dev(nan, F32), out)
+    torch.cuda.synchronize()
+    assert np.all(np.isnan(orc.bf16_to_f32(to_host(out, BF16))))
+
+
+@pytest.mark.parametrize("dt", [F32, BF16, F16])
+@pytest.mark.parametrize("n", [5, 4096, 100_003])
+def test_binary_same_shape_bitexact(orc, dev, dt, n):
+    say(f"binary dt={dt} n={n}")
+    a = orc.from_f32(orc.randn(n, seed=9), dt)
+    b = orc.from_f32(orc.randn(n, seed=10) + np.float32(4.0), dt)
+    ad, bd = to_dev(a, dt), to_dev(b, dt)
+    for op in range(4):
+        out = empty((n,), dt)
+        mbrt.binary(ad, bd, out, op)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(out, dt), orc.binary(a, b, dt, op), f"binary op {op}")
+    # in place a += b (residual add) and an unaligned (offset) view: scalar path
+    mbrt.binary(ad, bd, ad, 0)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(ad, dt), orc.binary(a, b, dt, 0), "in-place add")
+    if n > 1:
+        out = empty((n - 1,), dt)
+        mbrt.binary(to_dev(a, dt)[1:], to_dev(b, dt)[1:], out, 2)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(out, dt), orc.binary(a[1:].copy(), b[1:].copy(), dt, 2), "unaligned mul")
+
+
+def test_broadcast_and_scalar_ops(orc, dev):
+    say("broadcast binary / scalar / unary")
+    a = orc.randn((3, 1, 5, 7), seed=11)
+    b = orc.randn((4, 1, 7), seed=12)
+    out = empty((3, 4, 5, 7), F32)
+    mbrt.binary_broadcast(to_dev(a, F32), to_dev(b, F32), out, mbrt.MUL)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(out, F32), a * b, "broadcast mul")
+    x = orc.randn(1003, seed=13)
+    for op, a_, b_, ref in [(mbrt.SCALAR_ADD, 1.5, 0, x + np.float32(1.5)), (mbrt.SCALAR_MUL, -0.25, 0, x * np.float32(-0.25)),
+                            (mbrt.SCALAR_CLAMP, -0.5, 0.75, np.clip(x, -0.5, 0.75))]:
+        t = to_dev(x, F32)
+        mbrt.scalar_(t, op, a_, b_)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(t, F32), ref.astype(np.float32), f"scalar {op}")
+    out = empty((1003,), F32)
+    mbrt.unary(to_dev(x, F32), out, mbrt.UNARY_GT, 0.1)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(out, F32), (x > np.float32(0.1)).astype(np.float32), "gt")
+    mbrt.unary(to_dev(x, F32), out, mbrt.UNARY_NEG)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(out, F32), -x, "neg")
+
+
+def test_reductions(orc, dev):
+    say("reductions")
+    for shape in [(7, 801), (3, 5000), (100, 1)]:
+        x = orc.randn(shape, seed=14)
+        out = empty(shape[:-1], F32)
+        mbrt.reduce_last(to_dev(x, F32), out, mbrt.REDUCE_SUM)
+        torch.cuda.synchronize()
+        assert_close(to_host(out, F32), orc.reduce_last(x, 0), F32, "sum last", rtol=1e-5)
+        mbrt.reduce_last(to_dev(x, F32), out, mbrt.REDUCE_MAX)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(out, F32), x.max(-1), "max last")
+    x = orc.randn((6, 33, 10), seed=15)
+    for op in (0, 1):
+        out = empty((6, 10), F32)
+        mbrt.reduce_general(to_dev(x, F32), out, 1, op)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(out, F32), orc.reduce_general(x, 1, op), f"general reduce {op}")
+
+
+# ---- normalisation ------------------------------------------------------------------------
+
+def test_residual_rmsnorm_bl1_full(orc, dev):
+    say("BL-1 residual + RMSNorm f32 [48060,384]")
+    D = 384
+    x = inp(orc, (48060, D), SEED[1], 1)
+    r = inp(orc, (48060, D), SEED[1], 2)
+    g = inp(orc, (D,), SEED[1], 3, mean=1.0, std=0.02)
+    xd, rd, gd = to_dev(x, F32), to_dev(r, F32), to_dev(g, F32)
+    s, y = empty((48060, D), F32), empty((48060, D), F32)
+    mbrt.residual_add_rms_norm(xd, rd, gd, s, y, scale=float(np.sqrt(D)), eps=1e-8)
+    torch.cuda.synchronize()
+    ref_y, ref_s = orc.rms_norm(x, F32, g, F32, F32, float(np.sqrt(D)), 1e-8, res=r, sdt=F32, want_sum=True)
+    assert_bitexact(to_host(s, F32), ref_s, "residual sum")
+    err = assert_close(to_host(y, F32), ref_y, F32, "normed")
+    print("BL-1 errors", err)
+    # in place: residual <- residual + update
+    mbrt.residual_add_rms_norm(xd, rd, gd, xd, y, scale=float(np.sqrt(D)), eps=1e-8)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(xd, F32), ref_s, "in-place residual")
+    assert_close(to_host(y, F32), ref_y, F32, "in-place normed")
+
+
+@pytest.mark.parametrize("D", [8, 96, 256, 384, 1024, 4096, 100, 5000])
+@pytest.mark.parametrize("xdt,gdt,odt", [(F32, F32, F32), (BF16, F32, BF16), (BF16, BF16, BF16), (F32, F32, BF16),
+                                         (F16, F32, F16), (BF16, F32, F32)])
+def test_rmsnorm_shapes_dtypes(orc, dev, D, xdt, gdt, odt):
+    say(f"rms_norm D={D} {xdt},{gdt}->{odt}")
+    rows = 37
+    x = inp(orc, (rows, D), 99, D, xdt)
+    g = inp(orc, (D,), 98, D, gdt, mean=1.0, std=0.02)
+    y = empty((rows, D), odt)
+    mbrt.rms_norm(to_dev(x, xdt), to_dev(g, gdt), y, scale=float(np.sqrt(D)), eps=1e-12)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), orc.rms_norm(x, xdt, g, gdt, odt, float(np.sqrt(D)), 1e-12), odt, "rms")
+    if xdt == BF16:  # bf16 residual path: the sum is rounded to bf16 before normalising
+        r = inp(orc, (rows, D), 97, D, xdt)
+        s, y = empty((rows, D), BF16), empty((rows, D), odt)
+        mbrt.residual_add_rms_norm(to_dev(x, xdt), to_dev(r, xdt), to_dev(g, gdt), s, y, float(np.sqrt(D)), 1e-12)
+        torch.cuda.synchronize()
+        ry, rs = orc.rms_norm(x, xdt, g, gdt, odt, float(np.sqrt(D)), 1e-12, res=r, sdt=BF16, want_sum=True)
+        assert_bitexact(to_host(s, BF16), rs, "bf16 residual sum")
+        assert_close(to_host(y, odt), ry, odt, "bf16 residual normed")
+
+
+# ---- activations ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("act", [mbrt.ACT_GELU_REF, mbrt.ACT_GELU_STD])
+def test_gelu_bl2a_full(orc, dev, act):
+    say(f"BL-2a GELU act={act} bf16 [48060,1536]")
+    x = inp(orc, (48060, 1536), SEED[2], 1, BF16, std=1.5)
+    y = empty((48060, 1536), BF16)
+    mbrt.bias_act(to_dev(x, BF16), None, y, act)
+    torch.cuda.synchronize()
+    err = assert_close(to_host(y, BF16), orc.bias_act(x, BF16, None, F32, BF16, act), BF16, "gelu")
+    print("BL-2a errors", err)
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("xdt,odt", [(F32, F32), (BF16, BF16), (F32, BF16), (F16, F16)])
+def test_bias_act(orc, dev, act, xdt, odt):
+    say(f"bias_act act={act} {xdt}->{odt}")
+    x = inp(orc, (129, 264), 21, act, xdt, std=2.0)
+    b = inp(orc, (264,), 22, act)
+    for bias in (None, b):
+        y = empty((129, 264), odt)
+        mbrt.bias_act(to_dev(x, xdt), to_dev(bias, F32) if bias is not None else None, y, act)
+        torch.cuda.synchronize()
+        assert_close(to_host(y, odt), orc.bias_act(x, xdt, bias, F32, odt, act), odt, f"act {act} bias={bias is not None}")
+    xo = inp(orc, (1001,), 23, act, xdt)  # n % 8 != 0, no bias: vector body + tail
+    y = empty((1001,), odt)
+    mbrt.bias_act(to_dev(xo, xdt), None, y, act)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), orc.bias_act(xo, xdt, None, F32, odt, act), odt, "tail")
+
+
+def test_glu_bl2b_full(orc, dev):
+    say("BL-2b GLU bf16 [48060,3072]")
+    x = inp(orc, (48060, 3072), SEED[2], 2, BF16, std=1.5)
+    y = empty((48060, 1536), BF16)
+    mbrt.glu(to_dev(x, BF16), y)
+    torch.cuda.synchronize()
+    print("BL-2b errors", assert_close(to_host(y, BF16), orc.glu(x, BF16, BF16), BF16, "glu"))
+
+
+@pytest.mark.parametrize("half,xdt,odt", [(20, F32, F32), (7, BF16, BF16), (64, F32, BF16), (24, F16, F16)])
+def test_glu_shapes(orc, dev, half, xdt, odt):
+    say(f"glu half={half}")
+    x = inp(orc, (33, 2 * half), 24, half, xdt, std=1.5)
+    y = empty((33, half), odt)
+    mbrt.glu(to_dev(x, xdt), y)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), orc.glu(x, xdt, odt), odt, "glu")
+
+
+def test_gate_merge_bl2c_full(orc, dev):
+    say("BL-2c sigmoid gate merge bf16 attn [60,8,801,64]")
+    B, H, N, D = 60, 8, 801, 64
+    attn = inp(orc, (B, H, N, D), SEED[2], 3, BF16)
+    gate = inp(orc, (B, N, H), SEED[2], 4, BF16, std=2.0)
+    y = empty((B, N, H * D), BF16)
+    mbrt.gate_merge(to_dev(attn, BF16), to_dev(gate, BF16), y, mbrt.LAYOUT_BHND)
+    torch.cuda.synchronize()
+    ref = orc.gate_merge(attn, BF16, gate, BF16, BF16, B, H, N, D, layout=0)
+    print("BL-2c errors", assert_close(to_host(y, BF16), ref, BF16, "gate merge"))
+    attn_t = np.ascontiguousarray(attn.transpose(0, 2, 1, 3))
+    mbrt.gate_merge(to_dev(attn_t, BF16), to_dev(gate, BF16), y, mbrt.LAYOUT_BNHD)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, BF16), ref, BF16, "gate merge token-major")
+
+
+@pytest.mark.parametrize("D,adt,gdt,odt,logit", [(64, F32, F32, F32, True), (12, BF16, F32, BF16, True),
+                                                 (16, F32, BF16, F32, False), (64, F16, F16, F16, True)])
+def test_gate_merge_variants(orc, dev, D, adt, gdt, odt, logit):
+    say(f"gate merge D={D}")
+    B, H, N = 3, 4, 19
+    attn = inp(orc, (B, H, N, D), 25, D, adt)
+    gate = inp(orc, (B, N, H), 26, D, gdt, std=2.0)
+    y = empty((B, N, H * D), odt)
+    mbrt.gate_merge(to_dev(attn, adt), to_dev(gate, gdt), y, mbrt.LAYOUT_BHND, gate_is_logit=logit)
+    torch.cuda.synchronize()
+    ref = orc.gate_merge(attn, adt, gate, gdt, odt, B, H, N, D, layout=0, logit=logit)
+    assert_close(to_host(y, odt), ref, odt, "gate merge")
+
+
+# ---- softmax -------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(480, 801, 801), (6408, 60, 60)])
+@pytest.mark.parametrize("dt", [F32, BF16])
+def test_softmax_bl3_full(orc, dev, shape, dt):
+    say(f"BL-3 softmax {shape} dt={dt}")
+    rows, cols = shape[0] * shape[1], shape[2]
+    g = torch.Generator(device="cuda").manual_seed(SEED[3])
+    x = (torch.randn((rows, cols), generator=g, device="cuda") * 3.0).to(torch.float32 if dt == F32 else torch.bfloat16)
+    y = torch.empty_like(x)
+    mbrt.softmax(x, y, 1.0)
+    torch.cuda.synchronize()
+    # every row sums to 1 (whole tensor), oracle parity on sampled rows
+    sums = y.float().sum(-1, dtype=torch.float64)
+    tol = 1e-5 if dt == F32 else 2e-2
+    assert float((sums - 1).abs().max()) < tol
+    sel = np.random.default_rng(3).choice(rows, 2000, replace=False)
+    sel.sort()
+    seld = torch.from_numpy(sel).cuda()
+    xs, ys = to_host(x[seld], dt), to_host(y[seld], dt)
+    print("BL-3 errors", assert_close(ys, orc.softmax(xs, dt, dt, 1.0), dt, "softmax"))
+    # in place (same dtype) gives identical bits
+    mbrt.softmax(x, x, 1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(x.view(torch.int16 if dt != F32 else torch.int32), y.view(torch.int16 if dt != F32 else torch.int32))
+
+
+@pytest.mark.parametrize("cols", [1, 5, 8, 60, 63, 64, 65, 127, 801, 1301, 2048, 4096, 9000])
+@pytest.mark.parametrize("idt,odt", [(F32, F32), (BF16, BF16), (F32, BF16), (BF16, F32), (F16, F16)])
+def test_softmax_shapes(orc, dev, cols, idt, odt):
+    say(f"softmax cols={cols} {idt}->{odt}")
+    rows = 23
+    x = inp(orc, (rows, cols), 31, cols, idt, std=3.0)
+    y = empty((rows, cols), odt)
+    mbrt.softmax(to_dev(x, idt), y, 0.125)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), orc.softmax(x, idt, odt, 0.125), odt, "softmax")
+
+
+# ---- rotary --------------------------------------------------------------------------------
+
+def test_rotary_bl4a_full(orc, dev):
+    say("BL-4a rotary bf16 q,k [480,801,64], f32 tables [801,32]")
+    BH, N, D = 480, 801, 64
+    q = inp(orc, (BH, N, D), SEED[4], 2, BF16)
+    k = inp(orc, (BH, N, D), SEED[4], 3, BF16)
+    cos, sin = orc.rotary_tables(N, D)
+    qd, kd = to_dev(q, BF16), to_dev(k, BF16)
+    mbrt.rotary_(qd, kd, to_dev(cos, F32), to_dev(sin, F32), mbrt.LAYOUT_BHND)
+    torch.cuda.synchronize()
+    rq, rk = orc.rotary(q, k, BF16, cos, sin, F32, N, 1, layout=0)
+    print("BL-4a errors", assert_close(to_host(qd, BF16), rq, BF16, "rotary q"))
+    assert_close(to_host(kd, BF16), rk, BF16, "rotary k")
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("dt,tdt,D", [(F32, F32, 64), (BF16, BF16, 64), (F32, F32, 6), (F16, F32, 32)])
+def test_rotary_variants(orc, dev, layout, dt, tdt, D):
+    say(f"rotary layout={layout} dt={dt} tdt={tdt} D={D}")
+    B, H, N = 2, 3, 61
+    shape = (B * H, N, D) if layout == 0 else (B, N, H, D)
+    q = inp(orc, shape, 32, D, dt)
+    cos, sin = orc.rotary_tables(N, D)
+    if tdt == BF16:
+        cos, sin = orc.f32_to_bf16(cos), orc.f32_to_bf16(sin)
+    qd = to_dev(q, dt)
+    mbrt.rotary_(qd, None, to_dev(cos, tdt), to_dev(sin, tdt), layout, heads=H)
+    torch.cuda.synchronize()
+    rq, _ = orc.rotary(q, None, dt, cos, sin, tdt, N, H, layout=layout)
+    assert_close(to_host(qd, dt), rq, dt, "rotary")
+
+
+@pytest.mark.parametrize("N,out_n,idt,odt", [(60, 64, BF16, BF16), (801, 801, BF16, BF16), (17, 17, F32, F32),
+                                             (60, 60, F32, BF16)])
+def test_split_qkv_rotary(orc, dev, N, out_n, idt, odt):
+    say(f"split_qkv N={N} out_n={out_n}")
+    B, H, D = 2, 8, 64
+    qkv = inp(orc, (B, N, 3 * H * D), 33, N, idt)
+    cos, sin = orc.rotary_tables(N, D)
+    q, k, v = (empty((B, H, out_n, D), odt) for _ in range(3))
+    for t in (q, k, v):
+        t.fill_(float("nan"))
+    mbrt.split_qkv_rotary(to_dev(qkv, idt), to_dev(cos, F32), to_dev(sin, F32), q, k, v, H)
+    torch.cuda.synchronize()
+    rq, rk, rv = orc.split_qkv(qkv, idt, cos, sin, F32, odt, B, N, H, D, out_n)
+    assert_close(to_host(q, odt), rq, odt, "q")
+    assert_close(to_host(k, odt), rk, odt, "k")
+    assert_bitexact(to_host(v, odt), rv, "v")
+
+
+# ---- band split / merge ----------------------------------------------------------------------
+
+def _bands(orc):
+    return orc.mel_bands(44100.0, 2048, 60, 2)
+
+
+@pytest.mark.parametrize("idt,odt", [(I32, F32), (I64, F32), (I32, BF16)])
+def test_band_gather_bl5a_full(orc, dev, idt, odt):
+    say(f"BL-5a band gather B=4 idx={idt} out={odt}")
+    B, F, T = 4, 2050, 801
+    mb = _bands(orc)
+    stft = inp(orc, (B, F, T, 2), SEED[5], 1)
+    idx = mb["freq_indices"].astype(np.int64 if idt == I64 else np.int32)
+    out = empty((B, T, idx.size * 2), odt)
+    mbrt.band_gather(to_dev(stft, F32), to_dev(idx, idt), out)
+    torch.cuda.synchronize()
+    ref = orc.band_gather(stft, mb["freq_indices"], odt, B, F, T)
+    assert_bitexact(to_host(out, odt), ref, "gather")
+
+
+def test_band_merge_bl5b_full(orc, dev):
+    say("BL-5b mask merge B=4, 1 stem, f32")
+    B, F, T = 4, 2050, 801
+    mb = _bands(orc)
+    J = mb["freq_indices"].size
+    stft = inp(orc, (B, F, T, 2), SEED[5], 1)
+    mask = inp(orc, (B, T, J * 2), SEED[5], 2, std=0.5)
+    cnt = mb["bands_per_freq"].astype(np.float32)
+    out = empty((B * 2, F // 2, T, 2), F32)
+    sd = to_dev(stft, F32)
+    offd, indd, cntd = to_dev(mb["csr_offsets"], I32), to_dev(mb["csr_indices"], I32), to_dev(cnt, F32)
+    mbrt.band_mask_merge(sd, [to_dev(mask, F32)], offd, indd, cntd, out, 2)
+    torch.cuda.synchronize()
+    ref = orc.band_mask_merge(stft, [mask.reshape(B, T, J, 2)], F32, mb["csr_offsets"], mb["csr_indices"], cnt, F32, F32,
+                              B, F, T, 2)
+    print("BL-5b errors", assert_close(to_host(out, F32), ref, F32, "merge"))
+    # gather then merge with mask 1+0j is the identity on every bin (bit-exact, counts 1 and 2)
+    g = empty((B, T, J * 2), F32)
+    mbrt.band_gather(sd, to_dev(mb["freq_indices"], I32), g)
+    ones = torch.zeros((B, T, J, 2), device="cuda")
+    ones[..., 0] = 1
+    mbrt.band_mask_merge(sd, [ones.reshape(B, T, J * 2)], offd, indd, cntd, out, 2)
+    torch.cuda.synchronize()
+    ident = stft.reshape(B, F // 2, 2, T, 2).transpose(0, 2, 1, 3, 4).reshape(B * 2, F // 2, T, 2)
+    assert_bitexact(to_host(out, F32), np.ascontiguousarray(ident), "merge(mask=1) identity")
+
+
+@pytest.mark.parametrize("mdt,cdt,odt,S,idt", [(F32, F32, F32, 2, I32), (BF16, BF16, BF16, 2, I64),
+                                               (BF16, F32, F32, 1, I32)])
+def test_band_merge_variants(orc, dev, mdt, cdt, odt, S, idt):
+    say(f"band merge mdt={mdt} cdt={cdt} odt={odt} S={S}")
+    B, F, T = 2, 2050, 77
+    mb = _bands(orc)
+    J = mb["freq_indices"].size
+    stft = inp(orc, (B, F, T, 2), 41, S)
+    masks = [inp(orc, (B, T, J * 2), 42, s, mdt, std=0.5) for s in range(S)]
+    cnt = orc.from_f32(mb["bands_per_freq"].astype(np.float32), cdt)
+    out = empty((B * S * 2, F // 2, T, 2), odt)
+    ity = np.int64 if idt == I64 else np.int32
+    mbrt.band_mask_merge(to_dev(stft, F32), [to_dev(m, mdt) for m in masks], to_dev(mb["csr_offsets"].astype(ity), idt),
+                         to_dev(mb["csr_indices"].astype(ity), idt), to_dev(cnt, cdt), out, 2)
+    torch.cuda.synchronize()
+    ref = orc.band_mask_merge(stft, [m.reshape(B, T, J, 2) for m in masks], mdt, mb["csr_offsets"], mb["csr_indices"],
+                              cnt, cdt, odt, B, F, T, 2)
+    assert_close(to_host(out, odt), ref, odt, "merge")
+
+
+def test_band_merge_many_bands_per_freq(orc, dev):
+    say("band merge with up to 70 bands per freq (chunked CSR)")
+    # synthetic layout: 3 wide overlapping "bands" over a few freqs -> long CSR lists
+    B, F, T, C = 1, 40, 70, 1
+    fi = np.concatenate([np.arange(0, 40), np.arange(5, 35), np.repeat(np.arange(10, 12), 35)]).astype(np.int32)
+    J = fi.size
+    by = [[] for _ in range(F)]
+    for j, f in enumerate(fi):
+        by[f].append(j)
+    off = np.zeros(F + 1, np.int32)
+    off[1:] = np.cumsum([len(b) for b in by])
+    ind = np.array([j for b in by for j in b], np.int32)
+    cnt = np.array([len(b) for b in by], np.float32)
+    stft = inp(orc, (B, F, T, 2), 43, 0)
+    mask = inp(orc, (B, T, J * 2), 43, 1)
+    out = empty((B * C, F, T, 2), F32)
+    mbrt.band_mask_merge(to_dev(stft, F32), [to_dev(mask, F32)], to_dev(off, I32), to_dev(ind, I32), to_dev(cnt, F32),
+                         out, C)
+    torch.cuda.synchronize()
+    ref = orc.band_mask_merge(stft, [mask.reshape(B, T, J, 2)], F32, off, ind, cnt, F32, F32, B, F, T, C)
+    assert_close(to_host(out, F32), ref, F32, "merge chunked")
+
+
+def test_zero_dc(orc, dev):
+    say("zero_dc")
+    for dt in (F32, BF16):
+        x = inp(orc, (8, 1025, 33, 2), 44, dt, dt)
+        xd = to_dev(x, dt)
+        mbrt.zero_dc(xd)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(xd, dt), orc.zero_dc(x, dt), "zero_dc")

@@ -1,0 +1,364 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU kernels' checker.
+
+Each oracle function is checked against something that does not share its code:
+closed forms and invariants, brute force, numpy / torch (CPU, float64) formulations of
+the same maths, and the reference's own recorded band layout (tests/golden/).  Each
+check is chosen so that a plausible mistake (a dropped term, a wrong sign or index, a
+transposed operand, a wrong rounding) fails it.
+"""
+from __future__ import annotations
+
+import json
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from parity import BF16, F16, F32, assert_bitexact, assert_close
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---- rounding ----------------------------------------------------------------------------
+
+def test_bf16_roundtrip_all_patterns(orc):
+    bits = np.arange(65536, dtype=np.uint16)
+    f = orc.bf16_to_f32(bits)
+    assert np.array_equal(f.view(np.uint32) >> 16, bits.astype(np.uint32))
+    back = orc.f32_to_bf16(f)
+    nan = np.isnan(f)
+    assert np.array_equal(back[~nan], bits[~nan])
+    assert np.all(np.isnan(orc.bf16_to_f32(back[nan])))
+
+
+def test_f32_to_bf16_matches_torch(orc):
+    rng = np.random.default_rng(1)
+    u = rng.integers(0, 2**32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    # crafted ties: low 16 bits exactly 0x8000 with even and odd kept halves
+    ties = (rng.integers(0, 2**16, size=2000, dtype=np.uint32) << 16) | 0x8000
+    u = np.concatenate([u, ties, np.array([0x7f7fffff, 0x7f7f8000, 0xff7f8000, 0x00008000, 0x80018000],
+                                          dtype=np.uint32)])
+    f = u.view(np.float32)
+    f = f[~np.isnan(f)]
+    ours = orc.f32_to_bf16(f)
+    ref = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert_bitexact(ours, ref, "f32->bf16")
+
+
+def test_f16_conversions_match_numpy(orc):
+    bits = np.arange(65536, dtype=np.uint16)
+    ours = orc.f16_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    ok = ~np.isnan(ref)
+    assert_bitexact(ours[ok], ref[ok], "f16->f32")
+    rng = np.random.default_rng(2)
+    f = np.concatenate([
+        rng.standard_normal(100_000).astype(np.float32) * np.float32(1000),
+        rng.standard_normal(20_000).astype(np.float32) * np.float32(1e-5),  # subnormal range
+        np.array([65504, 65519.99, 65520, 1e6, 2**-24, 2**-25, 2**-25 * 1.0000001, 3 * 2**-26], np.float32),
+    ])
+    assert_bitexact(orc.f32_to_f16(f), f.astype(np.float16).view(np.uint16), "f32->f16")
+
+
+def _nearest_bf16_exact(v: float) -> int:
+    """Brute force: nearest bf16 to a double by exact rational comparison, ties to even."""
+    f = np.float32(v)
+    cands = set()
+    for base in (np.float32(f),):
+        b = int(np.array([base], np.float32).view(np.uint32)[0]) >> 16
+        for d in range(-2, 3):
+            cands.add((b + d) & 0xFFFF)
+    best = None
+    for c in cands:
+        cv = float(np.array([c << 16], np.uint32).view(np.float32)[0])
+        if not np.isfinite(cv):
+            continue
+        d = abs(Fraction(cv) - Fraction(v))
+        key = (d, c & 1)
+        if best is None or key < best[0]:
+            best = (key, c)
+    return best[1]
+
+
+def test_f64_to_bf16_single_rounding(orc):
+    rng = np.random.default_rng(3)
+    vals = list(rng.standard_normal(400) * 10.0 ** rng.integers(-30, 30, 400))
+    # exact midpoints between adjacent bf16 values, and a hair above/below them: a value
+    # rounded to f32 first would land on the midpoint and round to even wrongly.
+    for c in rng.integers(0x0080, 0x7f00, 200):
+        lo = float(np.array([int(c) << 16], np.uint32).view(np.float32)[0])
+        hi = float(np.array([(int(c) + 1) << 16], np.uint32).view(np.float32)[0])
+        mid = (lo + hi) / 2
+        vals += [mid, np.nextafter(mid, np.inf), np.nextafter(mid, -np.inf), -mid]
+    vals = np.array(vals, dtype=np.float64)
+    ours = orc.f64_to_bf16(vals)
+    ref = np.array([_nearest_bf16_exact(v) if v >= 0 else _nearest_bf16_exact(-v) | 0x8000 for v in vals],
+                   dtype=np.uint16)
+    assert_bitexact(ours, ref, "f64->bf16")
+
+
+def test_rng_deterministic_and_normal(orc):
+    a = orc.randn(1_000_001, seed=0x4D42520001, stream=3)
+    b = orc.randn(1_000_001, seed=0x4D42520001, stream=3)
+    c = orc.randn(1_000_001, seed=0x4D42520001, stream=4)
+    assert_bitexact(a, b, "rng determinism")
+    assert not np.array_equal(a, c)
+    assert abs(float(a.mean())) < 5e-3 and abs(float(a.std()) - 1.0) < 5e-3
+    s = orc.randn(200_000, seed=7, mean=1.0, std=0.02)
+    assert abs(float(s.mean()) - 1.0) < 5e-4 and abs(float(s.std()) - 0.02) < 5e-4
+
+
+# ---- tensor library --------------------------------------------------------------------
+
+@pytest.mark.parametrize("op", [0, 1, 2, 3])
+def test_binary_f32_matches_numpy_bitexact(orc, op):
+    a = orc.randn(10_001, seed=11)
+    b = orc.randn(10_001, seed=12) + np.float32(3.0)
+    ref = [np.add, np.subtract, np.multiply, np.divide][op](a, b)
+    assert_bitexact(orc.binary(a, b, F32, op), ref, f"binary op {op}")
+
+
+def test_binary_bf16_is_f32_op_then_rne(orc):
+    a = orc.f32_to_bf16(orc.randn(5000, seed=13))
+    b = orc.f32_to_bf16(orc.randn(5000, seed=14))
+    ref = torch.from_numpy((orc.bf16_to_f32(a) * orc.bf16_to_f32(b))).to(torch.bfloat16)
+    assert_bitexact(orc.binary(a, b, BF16, 2), ref.view(torch.int16).numpy().view(np.uint16), "bf16 mul")
+
+
+def test_broadcast_binary_matches_numpy(orc):
+    a = orc.randn((3, 1, 5, 7), seed=15)
+    b = orc.randn((4, 1, 7), seed=16)
+    out_shape = (3, 4, 5, 7)
+    sa = [35, 0, 7, 1]
+    sb = [0, 7, 0, 1]
+    assert_bitexact(orc.binary_broadcast(a, b, F32, out_shape, sa, sb, 0), a + b, "broadcast add")
+
+
+def test_strided_copy_permute_matches_numpy(orc):
+    x = orc.randn((4, 7, 6, 5), seed=17)
+    for perm in [(0, 2, 1, 3), (2, 0, 1, 3), (3, 1, 0, 2)]:
+        v = x.transpose(perm)
+        strides = [s // 4 for s in v.strides]
+        assert_bitexact(orc.strided_copy(x.reshape(-1), v.shape, strides), np.ascontiguousarray(v), str(perm))
+
+
+def test_index_select_and_pads(orc):
+    x = orc.randn((5, 9), seed=18)
+    idx = np.array([4, 0, 0, 8, 3], dtype=np.int64)
+    assert_bitexact(orc.index_select(x.reshape(-1), (5, 5), [9, 1], 1, idx), np.take(x, idx, axis=1), "take")
+    y = orc.pad(x, F32, (5, 14), [0, 2], value=-1.5)
+    assert_bitexact(y, np.pad(x, ((0, 0), (2, 3)), constant_values=-1.5), "pad const")
+    y = orc.pad(x, F32, (5, 14), [0, 3], reflect=True)
+    assert_bitexact(y, np.pad(x, ((0, 0), (3, 2)), mode="reflect"), "pad reflect")
+
+
+def test_reductions(orc):
+    x = orc.randn((6, 33, 10), seed=19)
+    got = orc.reduce_general(x, 1, 0)
+    acc = np.zeros((6, 10), np.float32)
+    for r in range(33):  # sequential f32 accumulation, the reference's loop order
+        acc = (acc + x[:, r, :]).astype(np.float32)
+    assert_bitexact(got, acc, "sequential sum")
+    assert_bitexact(orc.reduce_general(x, 1, 1), x.max(axis=1), "max")
+    assert_close(orc.reduce_last(x, 0), x.astype(np.float64).sum(-1).astype(np.float32), F32, "sum last")
+
+
+# ---- hot-path ops -------------------------------------------------------------------------
+
+def test_rms_norm_closed_forms_and_torch(orc):
+    D = 384
+    x = orc.randn((32, D), seed=21)
+    gamma_one = np.ones(D, np.float32)
+    y = orc.rms_norm(x, F32, gamma_one, F32, F32, scale=float(np.sqrt(D)), eps=0.0)
+    assert np.allclose(np.linalg.norm(y.astype(np.float64), axis=1), np.sqrt(D), rtol=1e-6)
+    y2 = orc.rms_norm(x * np.float32(8.0), F32, gamma_one, F32, F32, scale=float(np.sqrt(D)), eps=0.0)
+    assert_close(y2, y, F32, "scale invariance")
+    gamma = orc.randn(D, seed=22, mean=1.0, std=0.02)
+    y = orc.rms_norm(x, F32, gamma, F32, F32, scale=float(np.sqrt(D)), eps=1e-8)
+    xt = torch.from_numpy(x).double()
+    ref = xt * torch.rsqrt((xt * xt).sum(-1, keepdim=True) + 1e-8) * torch.from_numpy(gamma).double() * np.sqrt(D)
+    assert_close(y, ref.float().numpy(), F32, "rms vs torch")
+    # F.normalize form of the reference (src/mbr_cuda_tile.cu:4806-4812)
+    ref2 = torch.nn.functional.normalize(xt, dim=-1) * np.sqrt(D) * torch.from_numpy(gamma).double()
+    assert_close(y, ref2.float().numpy(), F32, "rms vs F.normalize")
+
+
+def test_residual_rms_sum_is_f32_add(orc):
+    D = 384
+    x = orc.randn((16, D), seed=23)
+    r = orc.randn((16, D), seed=24)
+    g = orc.randn(D, seed=25, mean=1.0, std=0.02)
+    out, s = orc.rms_norm(x, F32, g, F32, F32, scale=float(np.sqrt(D)), eps=1e-8, res=r, sdt=F32, want_sum=True)
+    assert_bitexact(s, x + r, "residual sum")
+    assert_close(out, orc.rms_norm(x + r, F32, g, F32, F32, float(np.sqrt(D)), 1e-8), F32, "normed")
+    xb, rb = orc.f32_to_bf16(x), orc.f32_to_bf16(r)
+    _, sb = orc.rms_norm(xb, BF16, g, F32, BF16, float(np.sqrt(D)), 1e-8, res=rb, sdt=BF16, want_sum=True)
+    assert_bitexact(sb, orc.f32_to_bf16(orc.bf16_to_f32(xb) + orc.bf16_to_f32(rb)), "bf16 residual sum")
+
+
+def test_activations_vs_torch(orc):
+    x = orc.randn((64, 96), seed=26, std=1.5)
+    xt = torch.from_numpy(x).double()
+    ref = {
+        1: 0.5 * xt * (1 + torch.erf(xt)),
+        2: torch.nn.functional.gelu(xt),
+        3: torch.sigmoid(xt),
+        4: torch.tanh(xt),
+    }
+    for act, r in ref.items():
+        assert_close(orc.bias_act(x, F32, None, F32, F32, act), r.float().numpy(), F32, f"act {act}")
+    # GELU(x) - GELU(-x) = x for both forms; GELU(0) = 0
+    for act in (1, 2):
+        z = np.array([0.0], np.float32)
+        assert orc.bias_act(z, F32, None, F32, F32, act)[0] == 0.0
+        d = orc.bias_act(x, F32, None, F32, F32, act).astype(np.float64) - \
+            orc.bias_act(-x, F32, None, F32, F32, act).astype(np.float64)
+        assert np.allclose(d, x, rtol=0, atol=1e-5)
+    # bias is added per column
+    b = orc.randn(96, seed=27)
+    assert_close(orc.bias_act(x, F32, b, F32, F32, 3), torch.sigmoid(xt + torch.from_numpy(b).double()).float().numpy(),
+                 F32, "bias sigmoid")
+
+
+def test_glu_and_gate_merge(orc):
+    x = orc.randn((10, 2 * 48), seed=28, std=1.5)
+    ref = torch.nn.functional.glu(torch.from_numpy(x).double(), dim=-1)
+    assert_close(orc.glu(x, F32, F32), ref.float().numpy(), F32, "glu")
+    x0 = x.copy()
+    x0[:, 48:] = 0
+    assert_bitexact(orc.glu(x0, F32, F32), x0[:, :48] * np.float32(0.5), "glu gate 0")
+    B, H, N, D = 2, 8, 5, 16
+    attn = orc.randn((B, H, N, D), seed=29)
+    gate = orc.randn((B, N, H), seed=30, std=2.0)
+    ref = torch.from_numpy(attn).double().permute(0, 2, 1, 3) * torch.sigmoid(torch.from_numpy(gate).double())[..., None]
+    got = orc.gate_merge(attn, F32, gate, F32, F32, B, H, N, D, layout=0)
+    assert_close(got, ref.reshape(B, N, H * D).float().numpy(), F32, "gate merge BHND")
+    attn_t = np.ascontiguousarray(attn.transpose(0, 2, 1, 3))
+    got2 = orc.gate_merge(attn_t, F32, gate, F32, F32, B, H, N, D, layout=1)
+    assert_bitexact(got2, got, "gate merge BNHD == BHND")
+
+
+def test_softmax(orc):
+    for cols in (801, 60, 7):
+        x = orc.randn((9, cols), seed=31 + cols, std=3.0)
+        for scale in (1.0, 0.125):
+            ref = torch.softmax(torch.from_numpy(x).double() * scale, dim=-1)
+            got = orc.softmax(x, F32, F32, scale)
+            assert_close(got, ref.float().numpy(), F32, f"softmax {cols} {scale}")
+            assert np.allclose(got.astype(np.float64).sum(-1), 1.0, atol=1e-6)
+        assert_close(orc.softmax(x + np.float32(5.0), F32, F32), orc.softmax(x, F32, F32), F32, "shift invariance",
+                     rtol=1e-4)
+
+
+def test_rotary_tables_and_apply(orc):
+    cos, sin = orc.rotary_tables(801, 64)
+    n = np.arange(801)[:, None].astype(np.float64)
+    i = np.arange(32)[None, :].astype(np.float64)
+    ang = n * 10000.0 ** (-2 * i / 64)
+    # the reference forms the angle in f32: |error| grows ~ n * 2^-24
+    assert np.max(np.abs(cos - np.cos(ang))) < 1e-4 and np.max(np.abs(sin - np.sin(ang))) < 1e-4
+    assert np.all(cos[0] == 1.0) and np.all(sin[0] == 0.0)
+    BH, N, D = 6, 801, 64
+    q = orc.randn((BH, N, D), seed=41)
+    k = orc.randn((BH, N, D), seed=42)
+    rq, rk = orc.rotary(q, k, F32, cos, sin, F32, N, 1, layout=0)
+    # complex formulation: (x0 + i x1) * (c + i s)
+    zc = torch.from_numpy(q).double().reshape(BH, N, 32, 2)
+    z = torch.complex(zc[..., 0], zc[..., 1]) * torch.complex(torch.from_numpy(cos).double(),
+                                                              torch.from_numpy(sin).double())
+    ref = torch.stack([z.real, z.imag], -1).reshape(BH, N, D)
+    assert_close(rq, ref.float().numpy(), F32, "rotary vs complex")
+    assert np.allclose(np.linalg.norm(rq.reshape(BH, N, 32, 2), axis=-1), np.linalg.norm(q.reshape(BH, N, 32, 2), axis=-1),
+                       rtol=1e-6)
+    assert_bitexact(rq[:, 0], q[:, 0], "identity at n=0")
+    # [B, N, H, D] layout rotates by position n = (row / H) % N
+    qb = np.ascontiguousarray(q.reshape(2, 3, N, D).transpose(0, 2, 1, 3))
+    rqb, _ = orc.rotary(qb, None, F32, cos, sin, F32, N, 3, layout=1)
+    assert_bitexact(rqb, np.ascontiguousarray(rq.reshape(2, 3, N, D).transpose(0, 2, 1, 3)), "BNHD == BHND")
+
+
+def test_split_qkv_matches_rotary(orc):
+    B, N, H, D = 2, 60, 8, 64
+    qkv = orc.randn((B, N, 3 * H * D), seed=43)
+    cos, sin = orc.rotary_tables(N, D)
+    q, k, v = orc.split_qkv(qkv, F32, cos, sin, F32, F32, B, N, H, D, 64)
+    parts = qkv.reshape(B, N, 3, H, D)
+    q_ref = np.ascontiguousarray(parts[:, :, 0].transpose(0, 2, 1, 3)).reshape(B * H, N, D)
+    rq, _ = orc.rotary(q_ref, None, F32, cos, sin, F32, N, 1)
+    assert_bitexact(q[:, :, :N].reshape(B * H, N, D), rq, "split q == rotary(q)")
+    assert_bitexact(v[:, :, :N], np.ascontiguousarray(parts[:, :, 2].transpose(0, 2, 1, 3)), "v copied")
+    assert np.all(q[:, :, N:] == 0) and np.all(k[:, :, N:] == 0) and np.all(v[:, :, N:] == 0)
+
+
+# ---- mel bands -----------------------------------------------------------------------------
+
+def test_mel_bands_match_reference_layout(orc):
+    gold = json.loads((GOLDEN / "mel_band_widths.json").read_text())
+    mb = orc.mel_bands(44100.0, 2048, 60, 2)
+    fpb = mb["freqs_per_band"]
+    widths = 4 * fpb
+    stems = gold["config"]["stems"]
+    want = {w: c // stems for w, c in gold["width_counts"]}
+    got = {}
+    for w in widths.tolist():
+        got[w] = got.get(w, 0) + 1
+    assert got == want, "band widths differ from the reference's recorded layout"
+    assert int(widths.sum()) == gold["mask_stride"] == 2 * mb["freq_indices"].size
+    assert mb["freq_indices"].size == 3958
+    bpf = mb["bands_per_freq"]
+    assert bpf.min() == 1 and bpf.max() == 2 and int((bpf[::2] == 1).sum()) == 71
+    # CSR: every band-bin appears once, ascending within a freq, pointing back at its freq
+    off, ind, fi = mb["csr_offsets"], mb["csr_indices"], mb["freq_indices"]
+    assert off[0] == 0 and off[-1] == ind.size and np.all(np.diff(off) == bpf)
+    assert np.array_equal(np.sort(ind), np.arange(ind.size))
+    for f in range(bpf.size):
+        seg = ind[off[f]:off[f + 1]]
+        assert np.all(np.diff(seg) > 0) and np.all(fi[seg] == f)
+    # stereo interleave 2*bin + ch, bands are contiguous bin ranges, DC and Nyquist covered
+    assert np.array_equal(fi[0::2] % 2, np.zeros(fi.size // 2)) and np.array_equal(fi[1::2], fi[0::2] + 1)
+    assert fi[0] == 0 and fi[-1] == 2049
+
+
+def test_band_gather_matches_numpy(orc):
+    B, F, T = 2, 2050, 37
+    stft = orc.randn((B, F, T, 2), seed=51)
+    idx = orc.mel_bands()["freq_indices"]
+    got = orc.band_gather(stft, idx, F32, B, F, T)
+    ref = stft[:, idx].transpose(0, 2, 1, 3).reshape(B, T, -1)
+    assert_bitexact(got, np.ascontiguousarray(ref), "gather")
+
+
+def test_band_merge_kat_and_numpy(orc):
+    B, F, T = 2, 2050, 19
+    mb = orc.mel_bands()
+    stft = orc.randn((B, F, T, 2), seed=52)
+    J = mb["freq_indices"].size
+    cnt = mb["bands_per_freq"].astype(np.float32)
+    ones = np.zeros((B, T, J, 2), np.float32)
+    ones[..., 0] = 1.0
+    out = orc.band_mask_merge(stft, [ones], F32, mb["csr_offsets"], mb["csr_indices"], cnt, F32, F32, B, F, T, 2)
+    # mask == 1+0j: sum over the freq's bands of s, divided by their count, is s exactly
+    ref = stft.reshape(B, F // 2, 2, T, 2).transpose(0, 2, 1, 3, 4).reshape(B * 2, F // 2, T, 2)
+    assert_bitexact(out, np.ascontiguousarray(ref), "merge KAT")
+    # general masks: scatter-add per band-bin with np.add.at in complex128, then / count
+    m = orc.randn((B, T, J, 2), seed=53, std=0.5)
+    m2 = orc.randn((B, T, J, 2), seed=54, std=0.5)
+    out = orc.band_mask_merge(stft, [m, m2], F32, mb["csr_offsets"], mb["csr_indices"], cnt, F32, F32, B, F, T, 2)
+    sc = stft[..., 0].astype(np.float64) + 1j * stft[..., 1]
+    for s, mm in enumerate([m, m2]):
+        mc = mm[..., 0].astype(np.float64) + 1j * mm[..., 1]            # [B, T, J]
+        acc = np.zeros((B, F, T), np.complex128)
+        prod = sc[:, mb["freq_indices"], :] * mc.transpose(0, 2, 1)      # [B, J, T]
+        np.add.at(acc, (slice(None), mb["freq_indices"]), prod)
+        acc /= cnt[None, :, None]
+        ref = np.stack([acc.real, acc.imag], -1).reshape(B, F // 2, 2, T, 2).transpose(0, 2, 1, 3, 4)
+        got = out.reshape(B, 2, 2, F // 2, T, 2)[:, s]
+        assert_close(np.ascontiguousarray(got), np.ascontiguousarray(ref).astype(np.float32), F32, f"merge stem {s}")
+
+
+def test_zero_dc(orc):
+    x = orc.randn((3, 5, 4, 2), seed=55)
+    y = orc.zero_dc(x, F32)
+    assert np.all(y[:, 0] == 0) and np.array_equal(y[:, 1:], x[:, 1:])
