@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace mbrt {
 
 enum DT : int { F32 = 0, F16 = 1, I64 = 2, BF16 = 3, I32 = 4 };
@@ -152,6 +154,20 @@ __device__ __forceinline__ void store4(void* p, int dt, int64_t e, const float (
     }
 }
 
+// VE consecutive elements at element e: VE = 4 (f32: one 16-byte access; 2-byte types:
+// 8 bytes) or VE = 8 (2-byte types: one 16-byte access; f32: two).  Kernels use VE = 4
+// whenever an f32 operand is involved so that lane l's bytes follow lane l-1's.
+template <int VE>
+__device__ __forceinline__ void vload(const void* p, int dt, int64_t e, float (&f)[VE]) {
+    if constexpr (VE == 4) load4(p, dt, e, f);
+    else load8(p, dt, e, f);
+}
+template <int VE>
+__device__ __forceinline__ void vstore(void* p, int dt, int64_t e, const float (&f)[VE]) {
+    if constexpr (VE == 4) store4(p, dt, e, f);
+    else store8(p, dt, e, f);
+}
+
 // ---- fast division by an invariant 32-bit divisor ------------------------------
 // Granlund & Montgomery, "Division by Invariant Integers using Multiplication" (1994),
 // round-up variant: q = (umulhi(n, m) + n) >> s with s = ceil(log2 d),
@@ -182,23 +198,140 @@ __device__ __forceinline__ void fdivmod(uint32_t n, const FastDiv& f, uint32_t& 
 }
 
 // ---- wave64 reductions -----------------------------------------------------------
-// Groups of G consecutive lanes (G in {1,2,4,8,16,32,64}) reduce together; every lane
-// of a group receives the group's result.  xor-butterfly through ds_swizzle/bpermute
-// is left to __shfl_xor, which the compiler lowers to DPP where the pattern allows.
+// Groups of G consecutive lanes (G in {1,2,4,8,16,32,64}) reduce together and every lane
+// of a group receives the group's result.  Steps within a 16-lane row are DPP operand
+// modifiers (quad_perm, row_half_mirror, row_mirror) fused into the add/max; the xor-16
+// step is a ds_swizzle (BitMode, within 32 lanes); the last step of a full wave reads
+// lanes 0 and 32 into scalar registers.  All 64 lanes must be active.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float swz_xor16(float v) {
+    // BitMode: and_mask 0x1f, or_mask 0, xor_mask 0x10 -> offset = (0x10 << 10) | 0x1f
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float lane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
 
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (G >= 2) v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]
+    if (G >= 4) v += dpp<0x4E>(v);    // quad_perm [2,3,0,1]
+    if (G >= 8) v += dpp<0x141>(v);   // row_half_mirror
+    if (G >= 16) v += dpp<0x140>(v);  // row_mirror
+    if (G >= 32) v += swz_xor16(v);
+    if (G >= 64) v = lane_f(v, 0) + lane_f(v, 32);
     return v;
 }
 
 template <int G>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if (G >= 2) v = fmaxf(v, dpp<0xB1>(v));
+    if (G >= 4) v = fmaxf(v, dpp<0x4E>(v));
+    if (G >= 8) v = fmaxf(v, dpp<0x141>(v));
+    if (G >= 16) v = fmaxf(v, dpp<0x140>(v));
+    if (G >= 32) v = fmaxf(v, swz_xor16(v));
+    if (G >= 64) v = fmaxf(lane_f(v, 0), lane_f(v, 32));
     return v;
 }
+
+// ---- dtype-templated vectors ------------------------------------------------------------
+// Vec<DT, VE> holds VE elements of dtype DT as raw registers: load/store move them with
+// one 8/16-byte (or two 16-byte) global access without touching the values, so a kernel
+// can issue every load before its first use; to_f32/from_f32 convert afterwards.
+
+template <int DT>
+struct DtSize {
+    static constexpr int value = DT == F32 ? 4 : 2;
+};
+
+template <int DT, int VE>
+struct Vec {
+    static constexpr int kBytes = VE * DtSize<DT>::value;
+    static constexpr int kWords = kBytes / 4;
+    uint32_t w[kWords];
+
+    __device__ __forceinline__ void load(const void* p, int64_t e) {
+        const char* b = reinterpret_cast<const char*>(p) + e * DtSize<DT>::value;
+        static_assert(kBytes == 4 || kBytes == 8 || kBytes % 16 == 0, "Vec: unsupported width");
+        if constexpr (kBytes == 4) {
+            w[0] = *reinterpret_cast<const uint32_t*>(b);
+        } else if constexpr (kBytes == 8) {
+            const u32x2 t = *reinterpret_cast<const u32x2*>(b);
+            w[0] = t.x; w[1] = t.y;
+        } else {
+#pragma unroll
+            for (int q = 0; q < kBytes / 16; ++q) {
+                const u32x4 t = reinterpret_cast<const u32x4*>(b)[q];
+                w[4 * q] = t.x; w[4 * q + 1] = t.y; w[4 * q + 2] = t.z; w[4 * q + 3] = t.w;
+            }
+        }
+    }
+    __device__ __forceinline__ void store(void* p, int64_t e) const {
+        char* b = reinterpret_cast<char*>(p) + e * DtSize<DT>::value;
+        if constexpr (kBytes == 4) {
+            *reinterpret_cast<uint32_t*>(b) = w[0];
+        } else if constexpr (kBytes == 8) {
+            *reinterpret_cast<u32x2*>(b) = u32x2{w[0], w[1]};
+        } else {
+#pragma unroll
+            for (int q = 0; q < kBytes / 16; ++q)
+                reinterpret_cast<u32x4*>(b)[q] = u32x4{w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]};
+        }
+    }
+    __device__ __forceinline__ void to_f32(float (&f)[VE]) const {
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) {
+            if constexpr (DT == F32) {
+                f[i] = __uint_as_float(w[i]);
+            } else if constexpr (DT == BF16) {
+                f[2 * i] = bf16_lo(w[i]);
+                f[2 * i + 1] = bf16_hi(w[i]);
+            } else {
+                const f32x2 t = unpack_f16x2(w[i]);
+                f[2 * i] = t.x;
+                f[2 * i + 1] = t.y;
+            }
+        }
+    }
+    __device__ __forceinline__ void from_f32(const float (&f)[VE]) {
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) {
+            if constexpr (DT == F32) w[i] = __float_as_uint(f[i]);
+            else if constexpr (DT == BF16) w[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+            else w[i] = pack_f16x2(f[2 * i], f[2 * i + 1]);
+        }
+    }
+};
+
+template <int DT>
+__device__ __forceinline__ float ld1(const void* p, int64_t i) {
+    if constexpr (DT == F32) return reinterpret_cast<const float*>(p)[i];
+    const uint32_t h = reinterpret_cast<const uint16_t*>(p)[i];
+    if constexpr (DT == BF16) return __uint_as_float(h << 16);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <int DT>
+__device__ __forceinline__ void st1(void* p, int64_t i, float v) {
+    if constexpr (DT == F32) reinterpret_cast<float*>(p)[i] = v;
+    else if constexpr (DT == BF16) reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+    else reinterpret_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v);
+}
+
+// Runs f(std::integral_constant<int, DT>) for a float dtype code known at run time.
+template <class Fn>
+__host__ __device__ __forceinline__ void with_dt(int dt, Fn f) {
+    if (dt == F32) f(std::integral_constant<int, F32>());
+    else if (dt == BF16) f(std::integral_constant<int, BF16>());
+    else f(std::integral_constant<int, F16>());
+}
+
+template <int DT>
+__host__ __device__ constexpr int ve_for() { return DT == F32 ? 4 : 8; }
 
 // ---- math ----------------------------------------------------------------------------
 
@@ -208,20 +341,29 @@ __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcp
 __device__ __forceinline__ float sigmoidf(float x) { return fast_rcp(1.0f + fast_exp(-x)); }
 
 // GELU in the reference's form 0.5 x (1 + erf(x)) (mode 1) and the standard
-// 0.5 x (1 + erf(x / sqrt 2)) (mode 2).
-__device__ __forceinline__ float gelu_ref(float x) { return 0.5f * x * (1.0f + erff(x)); }
-__device__ __forceinline__ float gelu_std(float x) {
-    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
-}
+// 0.5 x (1 + erf(x / sqrt 2)) (mode 2), both written as 0.5 x erfc(-z) so that the
+// negative tail keeps full relative precision (1 + erf(z) cancels for z << 0).
+__device__ __forceinline__ float gelu_ref(float x) { return 0.5f * x * erfcf(-x); }
+__device__ __forceinline__ float gelu_std(float x) { return 0.5f * x * erfcf(-x * 0.70710678118654752440f); }
 
-__device__ __forceinline__ float apply_act(float v, int act) {
-    switch (act) {
-        case 1: return gelu_ref(v);
-        case 2: return gelu_std(v);
-        case 3: return sigmoidf(v);
-        case 4: return tanhf(v);
-        default: return v;
-    }
+// erfc(-z) = 1 + erf(z) from Abramowitz & Stegun 7.1.26 (|error in erf| <= 1.5e-7):
+// q = (a1 t + ... + a5 t^5) exp(-z^2), t = 1 / (1 + p |z|) approximates erfc(|z|), so
+// 1 + erf(z) = q for z < 0 and 2 - q for z >= 0, with no cancellation in the tail.
+// Used where the result is rounded to bf16/f16 (8/11-bit significands).
+__device__ __forceinline__ float one_plus_erf_as(float z) {
+    const float az = fabsf(z);
+    const float t = fast_rcp(fmaf(0.3275911f, az, 1.0f));
+    float p = fmaf(1.061405429f, t, -1.453152027f);
+    p = fmaf(p, t, 1.421413741f);
+    p = fmaf(p, t, -0.284496736f);
+    p = fmaf(p, t, 0.254829592f);
+    p *= t;
+    const float q = p * __builtin_amdgcn_exp2f(-az * az * 1.44269504088896341f);
+    return z < 0.0f ? q : 2.0f - q;
+}
+__device__ __forceinline__ float gelu_ref_lowp(float x) { return 0.5f * x * one_plus_erf_as(x); }
+__device__ __forceinline__ float gelu_std_lowp(float x) {
+    return 0.5f * x * one_plus_erf_as(x * 0.70710678118654752440f);
 }
 
 }  // namespace mbrt

@@ -1,12 +1,15 @@
 // Activation kernels: bias + activation epilogue (GELU / sigmoid / tanh), GLU over the last
 // dim, and the fused sigmoid gate x head merge of the attention output.
 //
-// All three stream 8-element groups (16-byte accesses for 2-byte dtypes) and compute in
-// f32.  GLU reads the value and gate halves of a row as two coalesced streams.  The gate
-// merge reads the head-major attention output [B,H,N,D] in D-element runs (128 B at
-// D = 64 bf16), applies sigmoid(logit) once per (token, head) group and writes the merged
-// [B, N, H*D] rows contiguously: one pass instead of the reference's sigmoid epilogue
-// pass plus a separate merge pass (src/mbr_cuda_tile.cu:5504-5534 + 4752-4789).
+// The vector kernels are templated on their dtypes.  Each thread owns kU groups of VE
+// elements (16 bytes of the widest operand), issues all of its loads first (group index
+// clamped into the tensor, so no load is predicated), then computes in f32 and stores
+// with a predicate.  GLU reads the value and gate halves of a row as two coalesced
+// streams.  The gate merge reads the head-major attention output [B,H,N,D] in D-element
+// runs (128 B at D = 64 bf16), applies sigmoid(logit) once per (token, head) group and
+// writes the merged [B, N, H*D] rows contiguously: one pass instead of the reference's
+// sigmoid epilogue pass plus a separate merge pass (src/mbr_cuda_tile.cu:5504-5534 +
+// 4752-4789).  Unaligned operands take runtime-dtype element kernels.
 #include "abi_common.hpp"
 
 #include <algorithm>
@@ -15,7 +18,22 @@ namespace mbrt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kU = 2;  // 8-element groups per thread
+constexpr int kU = 2;        // groups per thread
+constexpr int kNoBias = -1;  // bias dtype tag: no bias
+
+__device__ __forceinline__ int64_t clamp_group(int64_t g, int64_t groups) { return g < groups ? g : groups - 1; }
+
+// GELU rounded to bf16/f16 uses the A&S 7.1.26 complement; f32 output uses erfcf.
+template <bool LOWP>
+__device__ __forceinline__ float act_fn(float v, int act) {
+    switch (act) {
+        case MBRT_ACT_GELU_REF: return LOWP ? gelu_ref_lowp(v) : gelu_ref(v);
+        case MBRT_ACT_GELU_STD: return LOWP ? gelu_std_lowp(v) : gelu_std(v);
+        case MBRT_ACT_SIGMOID: return sigmoidf(v);
+        case MBRT_ACT_TANH: return tanhf(v);
+        default: return v;
+    }
+}
 
 // ---- bias + activation ------------------------------------------------------------
 
@@ -24,68 +42,62 @@ struct BiasActArgs {
     const void* bias;  // may be NULL
     void* out;
     int xdt, bdt, odt;
-    int64_t n;          // rows * cols
-    int64_t groups;     // n / 8 (vector path)
-    FastDiv cols_div;   // cols (vector path with bias needs cols % 8 == 0)
+    int act;
+    int64_t n;         // rows * cols
     int64_t cols;
+    FastDiv cols_div;  // cols (vector path with bias needs cols % VE == 0 and n < 2^32)
 };
 
-template <int ACT>
-__device__ __forceinline__ float act_fn(float v) {
-    if (ACT == MBRT_ACT_GELU_REF) return gelu_ref(v);
-    if (ACT == MBRT_ACT_GELU_STD) return gelu_std(v);
-    if (ACT == MBRT_ACT_SIGMOID) return sigmoidf(v);
-    if (ACT == MBRT_ACT_TANH) return tanhf(v);
-    return v;
-}
-
-template <int ACT, bool HAS_BIAS>
+template <int XDT, int ODT, int BDT>
 __global__ __launch_bounds__(kThreads) void bias_act_vec_kernel(BiasActArgs a) {
+    constexpr int VE = (XDT == F32 || ODT == F32 || BDT == F32) ? 4 : 8;
+    constexpr bool LOWP = ODT != F32;
+    const int64_t groups = a.n / VE;
     const int64_t base = (int64_t)blockIdx.x * (kThreads * kU) + threadIdx.x;
+    if (groups > 0) {
+        Vec<XDT, VE> xv[kU];
+        Vec<(BDT == kNoBias ? F32 : BDT), VE> bv[kU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-        const int64_t g = base + u * kThreads;
-        if (g < a.groups) {
-            const int64_t e = g << 3;
-            float v[8];
-            load8(a.x, a.xdt, e, v);
-            if (HAS_BIAS) {
+        for (int u = 0; u < kU; ++u) {
+            const int64_t e = clamp_group(base + u * kThreads, groups) * VE;
+            xv[u].load(a.x, e);
+            if constexpr (BDT != kNoBias) {
                 const uint32_t col = (uint32_t)e - fdiv((uint32_t)e, a.cols_div) * a.cols_div.d;
-                float b[8];
-                load8(a.bias, a.bdt, col, b);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] += b[i];
+                bv[u].load(a.bias, col);
             }
+        }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = act_fn<ACT>(v[i]);
-            store8(a.out, a.odt, e, v);
+        for (int u = 0; u < kU; ++u) {
+            const int64_t g = base + u * kThreads;
+            if (g < groups) {
+                float v[VE];
+                xv[u].to_f32(v);
+                if constexpr (BDT != kNoBias) {
+                    float b[VE];
+                    bv[u].to_f32(b);
+#pragma unroll
+                    for (int i = 0; i < VE; ++i) v[i] += b[i];
+                }
+#pragma unroll
+                for (int i = 0; i < VE; ++i) v[i] = act_fn<LOWP>(v[i], a.act);
+                Vec<ODT, VE> o;
+                o.from_f32(v);
+                o.store(a.out, g * VE);
+            }
         }
     }
-    if (blockIdx.x == 0) {  // tail when n % 8 != 0 (only possible without bias)
-        const int64_t e = (a.groups << 3) + threadIdx.x;
-        if (e < a.n) store1(a.out, a.odt, e, act_fn<ACT>(load1(a.x, a.xdt, e)));
+    if (blockIdx.x == 0) {  // tail when n % VE != 0 (only possible without bias)
+        const int64_t e = groups * VE + threadIdx.x;
+        if (e < a.n) st1<ODT>(a.out, e, act_fn<LOWP>(ld1<XDT>(a.x, e), a.act));
     }
 }
 
-template <int ACT>
-__global__ __launch_bounds__(kThreads) void bias_act_scalar_kernel(BiasActArgs a) {
+__global__ __launch_bounds__(kThreads) void bias_act_elem_kernel(BiasActArgs a) {
     int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     for (; i < a.n; i += (int64_t)gridDim.x * kThreads) {
         float v = load1(a.x, a.xdt, i);
         if (a.bias != nullptr) v += load1(a.bias, a.bdt, i % a.cols);
-        store1(a.out, a.odt, i, act_fn<ACT>(v));
-    }
-}
-
-template <int ACT>
-void launch_bias_act(const BiasActArgs& a, bool vec, hipStream_t st) {
-    if (vec) {
-        const dim3 grid((unsigned)std::max<int64_t>(1, ceil_div(a.groups, (int64_t)kThreads * kU)));
-        if (a.bias != nullptr) hipLaunchKernelGGL((bias_act_vec_kernel<ACT, true>), grid, dim3(kThreads), 0, st, a);
-        else hipLaunchKernelGGL((bias_act_vec_kernel<ACT, false>), grid, dim3(kThreads), 0, st, a);
-    } else {
-        const dim3 grid((unsigned)std::min<int64_t>(ceil_div(a.n, kThreads), 1 << 20));
-        hipLaunchKernelGGL(bias_act_scalar_kernel<ACT>, grid, dim3(kThreads), 0, st, a);
+        store1(a.out, a.odt, i, a.odt == F32 ? act_fn<false>(v, a.act) : act_fn<true>(v, a.act));
     }
 }
 
@@ -96,30 +108,40 @@ struct GluArgs {
     void* out;
     int xdt, odt;
     int64_t rows, half;
-    int64_t groups;   // rows * half / 8
-    FastDiv gpr;      // groups per row = half / 8
+    int64_t groups;   // rows * half / VE
+    FastDiv gpr;      // groups per row = half / VE
 };
 
+template <int XDT, int ODT>
 __global__ __launch_bounds__(kThreads) void glu_vec_kernel(GluArgs a) {
+    constexpr int VE = (XDT == F32 || ODT == F32) ? 4 : 8;
     const int64_t base = (int64_t)blockIdx.x * (kThreads * kU) + threadIdx.x;
+    Vec<XDT, VE> xv[kU], gv[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        uint32_t row, c;
+        fdivmod((uint32_t)clamp_group(base + u * kThreads, a.groups), a.gpr, row, c);
+        const int64_t in0 = (int64_t)row * (2 * a.half) + (int64_t)c * VE;
+        xv[u].load(a.x, in0);
+        gv[u].load(a.x, in0 + a.half);
+    }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
         const int64_t g = base + u * kThreads;
         if (g < a.groups) {
-            uint32_t row, c;
-            fdivmod((uint32_t)g, a.gpr, row, c);
-            const int64_t in0 = (int64_t)row * (2 * a.half) + (int64_t)c * 8;
-            float v[8], gt[8];
-            load8(a.x, a.xdt, in0, v);
-            load8(a.x, a.xdt, in0 + a.half, gt);
+            float v[VE], gt[VE];
+            xv[u].to_f32(v);
+            gv[u].to_f32(gt);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = v[i] * sigmoidf(gt[i]);
-            store8(a.out, a.odt, g << 3, v);
+            for (int i = 0; i < VE; ++i) v[i] = v[i] * sigmoidf(gt[i]);
+            Vec<ODT, VE> o;
+            o.from_f32(v);
+            o.store(a.out, g * VE);
         }
     }
 }
 
-__global__ __launch_bounds__(kThreads) void glu_scalar_kernel(GluArgs a) {
+__global__ __launch_bounds__(kThreads) void glu_elem_kernel(GluArgs a) {
     const int64_t n = a.rows * a.half;
     int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     for (; i < n; i += (int64_t)gridDim.x * kThreads) {
@@ -139,45 +161,52 @@ struct GateArgs {
     int logit;
     int layout;
     int64_t B, H, N, D;
-    int64_t groups;    // B*N*H*D / 8
-    FastDiv gpt;       // groups per token = H*D/8
-    FastDiv gph;       // groups per head = D/8
+    int64_t groups;    // B*N*H*D / VE
+    FastDiv gpt;       // groups per token = H*D/VE
+    FastDiv gph;       // groups per head = D/VE
     FastDiv n_div;     // N
 };
 
-__device__ __forceinline__ float gate_value(const GateArgs& a, int64_t gi) {
-    float g = load1(a.gate, a.gdt, gi);
-    return a.logit ? sigmoidf(g) : g;
-}
-
+template <int ADT, int GDT, int ODT>
 __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
+    constexpr int VE = (ADT == F32 || ODT == F32) ? 4 : 8;
     const int64_t base = (int64_t)blockIdx.x * (kThreads * kU) + threadIdx.x;
+    Vec<ADT, VE> av[kU];
+    float gl[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        const uint32_t g = (uint32_t)clamp_group(base + u * kThreads, a.groups);
+        uint32_t token, rem, h, c;
+        fdivmod(g, a.gpt, token, rem);
+        fdivmod(rem, a.gph, h, c);
+        int64_t src;
+        if (a.layout == MBRT_LAYOUT_BHND) {
+            uint32_t b, n;
+            fdivmod(token, a.n_div, b, n);
+            src = (((int64_t)b * a.H + h) * a.N + n) * a.D + (int64_t)c * VE;
+        } else {
+            src = (int64_t)g * VE;
+        }
+        av[u].load(a.attn, src);
+        gl[u] = ld1<GDT>(a.gate, (int64_t)token * a.H + h);
+    }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
         const int64_t g = base + u * kThreads;
         if (g < a.groups) {
-            uint32_t token, rem, h, c;
-            fdivmod((uint32_t)g, a.gpt, token, rem);
-            fdivmod(rem, a.gph, h, c);
-            int64_t src;
-            if (a.layout == MBRT_LAYOUT_BHND) {
-                uint32_t b, n;
-                fdivmod(token, a.n_div, b, n);
-                src = (((int64_t)b * a.H + h) * a.N + n) * a.D + (int64_t)c * 8;
-            } else {
-                src = g << 3;
-            }
-            float v[8];
-            load8(a.attn, a.adt, src, v);
-            const float gv = gate_value(a, (int64_t)token * a.H + h);
+            float v[VE];
+            av[u].to_f32(v);
+            const float gv = a.logit ? sigmoidf(gl[u]) : gl[u];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] *= gv;
-            store8(a.out, a.odt, g << 3, v);
+            for (int i = 0; i < VE; ++i) v[i] *= gv;
+            Vec<ODT, VE> o;
+            o.from_f32(v);
+            o.store(a.out, g * VE);
         }
     }
 }
 
-__global__ __launch_bounds__(kThreads) void gate_merge_scalar_kernel(GateArgs a) {
+__global__ __launch_bounds__(kThreads) void gate_merge_elem_kernel(GateArgs a) {
     const int64_t n_total = a.B * a.N * a.H * a.D;
     int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     for (; i < n_total; i += (int64_t)gridDim.x * kThreads) {
@@ -191,9 +220,13 @@ __global__ __launch_bounds__(kThreads) void gate_merge_scalar_kernel(GateArgs a)
         } else {
             src = i;
         }
-        store1(a.out, a.odt, i, load1(a.attn, a.adt, src) * gate_value(a, token * a.H + h));
+        const float g = load1(a.gate, a.gdt, token * a.H + h);
+        store1(a.out, a.odt, i, load1(a.attn, a.adt, src) * (a.logit ? sigmoidf(g) : g));
     }
 }
+
+inline dim3 elem_grid(int64_t n) { return dim3((unsigned)std::min<int64_t>(std::max<int64_t>(1, ceil_div(n, kThreads)), 1 << 20)); }
+inline dim3 vec_grid(int64_t groups) { return dim3((unsigned)std::max<int64_t>(1, ceil_div(groups, (int64_t)kThreads * kU))); }
 
 }  // namespace
 }  // namespace mbrt
@@ -218,6 +251,7 @@ int mbrt_bias_act(const void* x, int x_dtype, const void* bias, int bias_dtype, 
     a.xdt = x_dtype;
     a.bdt = bias_dtype;
     a.odt = out_dtype;
+    a.act = act;
     a.n = rows * cols;
     a.cols = cols;
     if (a.n == 0) return MBRT_OK;
@@ -225,17 +259,23 @@ int mbrt_bias_act(const void* x, int x_dtype, const void* bias, int bias_dtype, 
     // In place with a wider output than input would overwrite unread input.
     MBRT_REQUIRE(x != out || dt_size(x_dtype) == dt_size(out_dtype), MBRT_E_INVALID_ARG,
                  "%s: in-place needs equal element sizes", op);
-    bool vec = aligned(x, 16) && aligned(out, 16) && (bias == nullptr || (aligned(bias, 16) && cols % 8 == 0)) &&
-               (bias == nullptr || a.n < (1ll << 32));
-    a.groups = a.n >> 3;
-    if (bias != nullptr && vec) a.cols_div = make_fastdiv((uint32_t)cols);
     hipStream_t st = as_stream(stream);
-    switch (act) {
-        case MBRT_ACT_GELU_REF: launch_bias_act<MBRT_ACT_GELU_REF>(a, vec, st); break;
-        case MBRT_ACT_GELU_STD: launch_bias_act<MBRT_ACT_GELU_STD>(a, vec, st); break;
-        case MBRT_ACT_SIGMOID: launch_bias_act<MBRT_ACT_SIGMOID>(a, vec, st); break;
-        case MBRT_ACT_TANH: launch_bias_act<MBRT_ACT_TANH>(a, vec, st); break;
-        default: launch_bias_act<MBRT_ACT_NONE>(a, vec, st); break;
+    const int ve = (x_dtype == F32 || out_dtype == F32 || (bias != nullptr && bias_dtype == F32)) ? 4 : 8;
+    const bool vec = aligned(x, 16) && aligned(out, 16) &&
+                     (bias == nullptr || (aligned(bias, 16) && cols % ve == 0 && a.n < (1ll << 32)));
+    if (vec) {
+        if (bias != nullptr) a.cols_div = make_fastdiv((uint32_t)cols);
+        const dim3 grid = vec_grid(a.n / ve);
+        with_dt(x_dtype, [&](auto xt) {
+            with_dt(out_dtype, [&](auto ot) {
+                constexpr int X = decltype(xt)::value, O = decltype(ot)::value;
+                if (bias == nullptr) hipLaunchKernelGGL((bias_act_vec_kernel<X, O, kNoBias>), grid, dim3(kThreads), 0, st, a);
+                else if (bias_dtype == F32) hipLaunchKernelGGL((bias_act_vec_kernel<X, O, F32>), grid, dim3(kThreads), 0, st, a);
+                else hipLaunchKernelGGL((bias_act_vec_kernel<X, O, BF16>), grid, dim3(kThreads), 0, st, a);
+            });
+        });
+    } else {
+        hipLaunchKernelGGL(bias_act_elem_kernel, elem_grid(a.n), dim3(kThreads), 0, st, a);
     }
     return check_launch(op);
 }
@@ -256,15 +296,19 @@ int mbrt_glu_last_dim(const void* x, int x_dtype, void* out, int out_dtype, int6
     a.rows = rows;
     a.half = half_dim;
     hipStream_t st = as_stream(stream);
-    const bool vec = half_dim % 8 == 0 && aligned(x, 16) && aligned(out, 16) && rows * half_dim / 8 < (1ll << 32);
+    const int ve = (x_dtype == F32 || out_dtype == F32) ? 4 : 8;
+    const bool vec = half_dim % ve == 0 && aligned(x, 16) && aligned(out, 16) && rows * half_dim / ve < (1ll << 32);
     if (vec) {
-        a.groups = rows * half_dim / 8;
-        a.gpr = make_fastdiv((uint32_t)(half_dim / 8));
-        hipLaunchKernelGGL(glu_vec_kernel, dim3((unsigned)ceil_div(a.groups, (int64_t)kThreads * kU)), dim3(kThreads),
-                           0, st, a);
+        a.groups = rows * half_dim / ve;
+        a.gpr = make_fastdiv((uint32_t)(half_dim / ve));
+        with_dt(x_dtype, [&](auto xt) {
+            with_dt(out_dtype, [&](auto ot) {
+                constexpr int X = decltype(xt)::value, O = decltype(ot)::value;
+                hipLaunchKernelGGL((glu_vec_kernel<X, O>), vec_grid(a.groups), dim3(kThreads), 0, st, a);
+            });
+        });
     } else {
-        hipLaunchKernelGGL(glu_scalar_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(rows * half_dim, kThreads), 1 << 20)),
-                           dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL(glu_elem_kernel, elem_grid(rows * half_dim), dim3(kThreads), 0, st, a);
     }
     return check_launch(op);
 }
@@ -295,18 +339,24 @@ int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const void* gate, 
     a.N = N;
     a.D = D;
     hipStream_t st = as_stream(stream);
-    const bool vec = D % 8 == 0 && aligned(attn, 16) && aligned(merged, 16) && total / 8 < (1ll << 32) &&
+    const int ve = (attn_dtype == F32 || out_dtype == F32) ? 4 : 8;
+    const bool vec = D % ve == 0 && aligned(attn, 16) && aligned(merged, 16) && total / ve < (1ll << 32) &&
                      B * N < (1ll << 31);
     if (vec) {
-        a.groups = total / 8;
-        a.gpt = make_fastdiv((uint32_t)(H * D / 8));
-        a.gph = make_fastdiv((uint32_t)(D / 8));
+        a.groups = total / ve;
+        a.gpt = make_fastdiv((uint32_t)(H * D / ve));
+        a.gph = make_fastdiv((uint32_t)(D / ve));
         a.n_div = make_fastdiv((uint32_t)N);
-        hipLaunchKernelGGL(gate_merge_vec_kernel, dim3((unsigned)ceil_div(a.groups, (int64_t)kThreads * kU)),
-                           dim3(kThreads), 0, st, a);
+        with_dt(attn_dtype, [&](auto at) {
+            with_dt(gate_dtype, [&](auto gt) {
+                with_dt(out_dtype, [&](auto ot) {
+                    constexpr int A = decltype(at)::value, G = decltype(gt)::value, O = decltype(ot)::value;
+                    hipLaunchKernelGGL((gate_merge_vec_kernel<A, G, O>), vec_grid(a.groups), dim3(kThreads), 0, st, a);
+                });
+            });
+        });
     } else {
-        hipLaunchKernelGGL(gate_merge_scalar_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(total, kThreads), 1 << 20)),
-                           dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL(gate_merge_elem_kernel, elem_grid(total), dim3(kThreads), 0, st, a);
     }
     return check_launch(op);
 }

@@ -46,39 +46,55 @@ struct GatherArgs {
     int64_t F, T, J;
 };
 
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / 64); }
+
+template <int ODT>
+__device__ __forceinline__ void store_complex(void* out, int64_t o, f32x2 v) {
+    if constexpr (ODT == F32) reinterpret_cast<f32x2*>(out)[o] = v;
+    else if constexpr (ODT == BF16) reinterpret_cast<uint32_t*>(out)[o] = pack_bf16x2(v.x, v.y);
+    else reinterpret_cast<uint32_t*>(out)[o] = pack_f16x2(v.x, v.y);
+}
+
+template <int MDT>
+__device__ __forceinline__ f32x2 load_complex(const void* p, int64_t i) {
+    if constexpr (MDT == F32) return reinterpret_cast<const f32x2*>(p)[i];
+    const uint32_t w = reinterpret_cast<const uint32_t*>(p)[i];
+    if constexpr (MDT == BF16) return f32x2{bf16_lo(w), bf16_hi(w)};
+    else return unpack_f16x2(w);
+}
+
+// Block (j-tile, t-tile, b).  Wave w reads tile rows jj = w, w+4, ..., w+60: the 64 frames
+// of stft row idx[j0+jj] (512 contiguous bytes).  The row index is loaded once per lane and
+// broadcast with readlane; indices are clamped into the tensors so the 16 loads of a lane
+// are unconditional and in flight together.
+template <int ODT>
 __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
     __shared__ f32x2 tile[kTJ][kTT + 1];
     const int64_t j0 = (int64_t)blockIdx.x * kTJ;
     const int64_t t0 = (int64_t)blockIdx.y * kTT;
     const int64_t b = blockIdx.z;
     const int lane = threadIdx.x % 64;
-    const int grp = threadIdx.x / 64;
-    const f32x2* stft = reinterpret_cast<const f32x2*>(a.stft) + b * a.F * a.T;
-    // read: row jj of the tile = stft[b, idx[j0+jj], t0 : t0+64]
-#pragma unroll 4
-    for (int jj = grp; jj < kTJ; jj += kThreads / 64) {
-        const int64_t j = j0 + jj, t = t0 + lane;
-        if (j < a.J && t < a.T) {
-            const int64_t f = load_index(a.idx, a.idx64, j);
-            tile[jj][lane] = stft[f * a.T + t];
-        }
+    const int w = wave_id();
+    const int f_lane = (int)load_index(a.idx, a.idx64, min(j0 + lane, a.J - 1));
+    const int64_t tq = min(t0 + lane, a.T - 1);
+    const f32x2* stft = reinterpret_cast<const f32x2*>(a.stft) + b * a.F * a.T + tq;
+    constexpr int kR = kTJ / (kThreads / 64);  // 16 rows per wave
+    f32x2 v[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+        const int64_t f = __builtin_amdgcn_readlane(f_lane, w + 4 * r);
+        v[r] = stft[f * a.T];
     }
+#pragma unroll
+    for (int r = 0; r < kR; ++r) tile[w + 4 * r][lane] = v[r];
     __syncthreads();
-    // write: out[b, t0+tt, j0 : j0+64]
-#pragma unroll 4
-    for (int tt = grp; tt < kTT; tt += kThreads / 64) {
-        const int64_t j = j0 + lane, t = t0 + tt;
-        if (j < a.J && t < a.T) {
-            const f32x2 v = tile[lane][tt];
-            const int64_t o = (b * a.T + t) * a.J + j;
-            if (a.odt == F32) {
-                reinterpret_cast<f32x2*>(a.out)[o] = v;
-            } else if (a.odt == BF16) {
-                reinterpret_cast<uint32_t*>(a.out)[o] = pack_bf16x2(v.x, v.y);
-            } else {
-                reinterpret_cast<uint32_t*>(a.out)[o] = pack_f16x2(v.x, v.y);
-            }
-        }
+    // write: out[b, t0+tt, j0 : j0+64] for tt = w, w+4, ...
+    const int64_t j = j0 + lane;
+    if (j >= a.J) return;
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+        const int tt = w + 4 * r;
+        if (t0 + tt < a.T) store_complex<ODT>(a.out, (b * a.T + t0 + tt) * a.J + j, tile[lane][tt]);
     }
 }
 
@@ -97,13 +113,12 @@ struct MergeArgs {
     int64_t F, T, J, C;
 };
 
-__device__ __forceinline__ f32x2 load_mask(const void* p, int mdt, int64_t i) {
-    if (mdt == F32) return reinterpret_cast<const f32x2*>(p)[i];
-    const uint32_t w = reinterpret_cast<const uint32_t*>(p)[i];
-    if (mdt == BF16) return f32x2{bf16_lo(w), bf16_hi(w)};
-    return unpack_f16x2(w);
-}
-
+// Block (t-tile, f-tile, b*S+s).  Wave w owns freqs f0+w, f0+w+4, ... (8 of them) and lane
+// t of the tile: its stft values and CSR ranges are loaded up front.  The CSR entries of
+// the tile's freqs are staged 64 at a time: lane e loads mask[b, t, ind[c0+e]] for 16
+// frames, the tile is transposed through LDS, and each thread sums its freqs' entries in
+// ascending order.  All loads use clamped indices and are unconditional.
+template <int MDT, int ODT>
 __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     __shared__ f32x2 ms[kME][kTT + 1];
     const int64_t t0 = (int64_t)blockIdx.x * kTT;
@@ -112,47 +127,39 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     const int64_t b = bs / a.S, s = bs - b * a.S;
     const void* mask = a.mask[s];
     const int lane = threadIdx.x % 64;
-    const int grp = threadIdx.x / 64;
-    constexpr int kPer = kTF / (kThreads / 64);  // freqs per thread (8)
+    const int w = wave_id();
+    constexpr int kPer = kTF / (kThreads / 64);  // freqs per wave (8)
+    constexpr int kR = kTT / (kThreads / 64);    // staged frames per wave (16)
     const int64_t t = t0 + lane;
-    const bool t_ok = t < a.T;
+    const int64_t tq = min(t, a.T - 1);
 
-    const int64_t f_end = f0 + kTF < a.F ? f0 + kTF : a.F;
+    const int64_t f_end = min(f0 + kTF, a.F);
     const int64_t e_begin = load_index(a.off, a.idx64, f0);
     const int64_t e_end = load_index(a.off, a.idx64, f_end);
 
-    // this thread's freqs: f0 + grp + 4*r
     f32x2 sv[kPer], acc[kPer];
     int64_t eb[kPer], ee[kPer];
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
-        const int64_t f = f0 + grp + 4 * r;
+        const int64_t f = min(f0 + w + 4 * r, a.F - 1);
+        eb[r] = load_index(a.off, a.idx64, f);
+        ee[r] = load_index(a.off, a.idx64, f + 1);
+        sv[r] = reinterpret_cast<const f32x2*>(a.stft)[(b * a.F + f) * a.T + tq];
         acc[r] = f32x2{0.0f, 0.0f};
-        eb[r] = ee[r] = 0;
-        sv[r] = f32x2{0.0f, 0.0f};
-        if (f < a.F) {
-            eb[r] = load_index(a.off, a.idx64, f);
-            ee[r] = load_index(a.off, a.idx64, f + 1);
-            if (t_ok) sv[r] = reinterpret_cast<const f32x2*>(a.stft)[(b * a.F + f) * a.T + t];
-        }
     }
-    const f32x2* mrow = nullptr;
-    (void)mrow;
     for (int64_t c0 = e_begin; c0 < e_end; c0 += kME) {
-        const int64_t c1 = c0 + kME < e_end ? c0 + kME : e_end;
-        // stage mask[b, t0 : t0+64, indices[c0 : c1]] as ms[e - c0][tt]
-        for (int tt = grp; tt < kTT; tt += kThreads / 64) {
-            const int64_t e = c0 + lane, tq = t0 + tt;
-            if (e < c1 && tq < a.T) {
-                const int64_t j = load_index(a.ind, a.idx64, e);
-                ms[lane][tt] = load_mask(mask, a.mdt, (b * a.T + tq) * a.J + j);
-            }
-        }
+        const int64_t c1 = min(c0 + kME, e_end);
+        const int64_t j = load_index(a.ind, a.idx64, min(c0 + lane, c1 - 1));
+        f32x2 mv[kR];
+#pragma unroll
+        for (int r = 0; r < kR; ++r) mv[r] = load_complex<MDT>(mask, (b * a.T + min(t0 + w + 4 * r, a.T - 1)) * a.J + j);
+#pragma unroll
+        for (int r = 0; r < kR; ++r) ms[lane][w + 4 * r] = mv[r];
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
-            const int64_t lo = eb[r] > c0 ? eb[r] : c0;
-            const int64_t hi = ee[r] < c1 ? ee[r] : c1;
+            if (f0 + w + 4 * r >= a.F) continue;
+            const int64_t lo = max(eb[r], c0), hi = min(ee[r], c1);
             for (int64_t e = lo; e < hi; ++e) {
                 const f32x2 m = ms[e - c0][lane];
                 acc[r].x += sv[r].x * m.x - sv[r].y * m.y;
@@ -161,25 +168,18 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
         }
         __syncthreads();
     }
-    if (!t_ok) return;
+    if (t >= a.T) return;
+    const int64_t bins = a.F / a.C;
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
-        const int64_t f = f0 + grp + 4 * r;
+        const int64_t f = f0 + w + 4 * r;
         if (f >= a.F) continue;
         float den = load1(a.cnt, a.cdt, f);
         den = den > 1.0e-8f ? den : 1.0e-8f;
         const float inv = 1.0f / den;
         const int64_t bin = f / a.C, ch = f - bin * a.C;
-        const int64_t bins = a.F / a.C;
         const int64_t o = (((b * a.S + s) * a.C + ch) * bins + bin) * a.T + t;
-        const float re = acc[r].x * inv, im = acc[r].y * inv;
-        if (a.odt == F32) {
-            reinterpret_cast<f32x2*>(a.out)[o] = f32x2{re, im};
-        } else if (a.odt == BF16) {
-            reinterpret_cast<uint32_t*>(a.out)[o] = pack_bf16x2(re, im);
-        } else {
-            reinterpret_cast<uint32_t*>(a.out)[o] = pack_f16x2(re, im);
-        }
+        store_complex<ODT>(a.out, o, f32x2{acc[r].x * inv, acc[r].y * inv});
     }
 }
 
@@ -215,7 +215,9 @@ int mbrt_band_gather(const float* stft, const void* freq_indices, int index_dtyp
     MBRT_REQUIRE(B <= 65535, MBRT_E_SHAPE, "%s: batch %lld exceeds 65535", op, (long long)B);
     GatherArgs a{stft, freq_indices, index_dtype == I64, out, out_dtype, total_freq, frames, n_band_freqs};
     const dim3 grid((unsigned)ceil_div(n_band_freqs, kTJ), (unsigned)ceil_div(frames, kTT), (unsigned)B);
-    hipLaunchKernelGGL(band_gather_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+    with_dt(out_dtype, [&](auto ot) {
+        hipLaunchKernelGGL(band_gather_kernel<decltype(ot)::value>, grid, dim3(kThreads), 0, as_stream(stream), a);
+    });
     return check_launch(op);
 }
 
@@ -255,7 +257,12 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
     a.J = n_band_freqs;
     a.C = channels;
     const dim3 grid((unsigned)ceil_div(frames, kTT), (unsigned)ceil_div(total_freq, kTF), (unsigned)(B * num_stems));
-    hipLaunchKernelGGL(band_merge_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+    with_dt(mask_dtype, [&](auto mt) {
+        with_dt(out_dtype, [&](auto ot) {
+            hipLaunchKernelGGL((band_merge_kernel<decltype(mt)::value, decltype(ot)::value>), grid, dim3(kThreads), 0,
+                               as_stream(stream), a);
+        });
+    });
     return check_launch(op);
 }
 

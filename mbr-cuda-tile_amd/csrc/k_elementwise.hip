@@ -1,10 +1,13 @@
 // Flat element-wise kernels of the tensor library (src/tensor_cuda_tile.cu:51-339 and the
 // broadcast binary of src/tensor_cuda_glue.cu:57-114).
 //
-// Every flat kernel streams 8-element groups with 16-byte (2-byte dtypes) or 2x16-byte
-// (f32) global accesses, U groups per thread, and handles the n % 8 tail with scalar
-// accesses in the same launch.  The broadcast binary replaces per-element 64-bit div/mod
-// over 8 dims with 32-bit multiply-shift division over the (merged) output dims.
+// The vector kernels are templated on the dtypes: every thread owns kU groups of VE
+// elements (16 bytes of its widest operand), issues all of its loads first (group indices
+// clamped into the array, so no load is predicated), then converts, computes and stores
+// with a predicate.  The n % VE tail is handled element-wise by block 0 in the same launch.
+// Operands that are not 16-byte aligned use runtime-dtype element kernels.  The broadcast
+// binary replaces per-element 64-bit div/mod over 8 dims with 32-bit multiply-shift
+// division over the (merged) output dims.
 #include "abi_common.hpp"
 
 #include <algorithm>
@@ -16,37 +19,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kU = 4;  // 8-element groups per thread
-
-inline int64_t flat_grid(int64_t groups) { return std::max<int64_t>(1, ceil_div(groups, (int64_t)kThreads * kU)); }
-
-// Iterates the 8-element groups and the scalar tail of an n-element array.
-// body8(e) handles elements [e, e+8); body1(e) a single element.  VEC = false (some
-// pointer not 16-byte aligned) runs body1 over every element with a grid-stride loop.
-template <bool VEC, class Body8, class Body1>
-__device__ __forceinline__ void flat_loop(int64_t n, Body8 body8, Body1 body1) {
-    if (VEC) {
-        const int64_t groups = n >> 3;
-        const int64_t base = (int64_t)blockIdx.x * (kThreads * kU) + threadIdx.x;
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            int64_t g = base + u * kThreads;
-            if (g < groups) body8(g << 3);
-        }
-        // tail: elements [groups*8, n) handled by the first threads of block 0
-        if (blockIdx.x == 0) {
-            int64_t e = (groups << 3) + threadIdx.x;
-            if (e < n) body1(e);
-        }
-    } else {
-        int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-        for (; i < n; i += (int64_t)gridDim.x * kThreads) body1(i);
-    }
-}
-
-// Grid for flat_loop<VEC>.
-inline int64_t flat_grid_for(bool vec, int64_t n) {
-    return vec ? flat_grid(n >> 3) : std::min<int64_t>(std::max<int64_t>(1, ceil_div(n, kThreads)), 1 << 20);
-}
 
 // ---- fill / arange ------------------------------------------------------------------
 
@@ -89,80 +61,115 @@ __global__ __launch_bounds__(kThreads) void arange_kernel(void* dst, int dt, int
     }
 }
 
-// ---- conversions --------------------------------------------------------------------
+// ---- typed vector kernels ---------------------------------------------------------------
 
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void convert_float_kernel(const void* src, int sdt, void* dst, int ddt,
-                                                          int64_t n) {
-    flat_loop<VEC>(
-        n,
-        [&](int64_t e) {
-            float f[8];
-            load8(src, sdt, e, f);
-            store8(dst, ddt, e, f);
-        },
-        [&](int64_t e) { store1(dst, ddt, e, load1(src, sdt, e)); });
+#define MBRT_FLAT_PROLOGUE(VE_)                                                   \
+    constexpr int VE = (VE_);                                                     \
+    const int64_t groups = n / VE;                                                \
+    const int64_t base = (int64_t)blockIdx.x * (kThreads * kU) + threadIdx.x;
+
+__device__ __forceinline__ int64_t clamp_group(int64_t g, int64_t groups) { return g < groups ? g : groups - 1; }
+
+template <int SDT, int DDT>
+__global__ __launch_bounds__(kThreads) void convert_vec_kernel(const void* src, void* dst, int64_t n) {
+    MBRT_FLAT_PROLOGUE((SDT == F32 || DDT == F32) ? 4 : 8)
+    if (groups > 0) {
+        Vec<SDT, VE> v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u].load(src, clamp_group(base + u * kThreads, groups) * VE);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t g = base + u * kThreads;
+            if (g < groups) {
+                float f[VE];
+                v[u].to_f32(f);
+                Vec<DDT, VE> o;
+                o.from_f32(f);
+                o.store(dst, g * VE);
+            }
+        }
+    }
+    if (blockIdx.x == 0) {
+        const int64_t e = groups * VE + threadIdx.x;
+        if (e < n) st1<DDT>(dst, e, ld1<SDT>(src, e));
+    }
 }
 
-// Conversions that involve an integer type (not on any hot path).
-__global__ __launch_bounds__(kThreads) void convert_int_kernel(const void* src, int sdt, void* dst, int ddt,
-                                                        int64_t n) {
-    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    for (; i < n; i += (int64_t)gridDim.x * kThreads) {
-        if (sdt == I64 || sdt == I32) {
-            int64_t v = sdt == I64 ? reinterpret_cast<const int64_t*>(src)[i]
-                                   : (int64_t)reinterpret_cast<const int32_t*>(src)[i];
-            if (ddt == I64) reinterpret_cast<int64_t*>(dst)[i] = v;
-            else if (ddt == I32) reinterpret_cast<int32_t*>(dst)[i] = (int32_t)v;
-            else store1(dst, ddt, i, (float)v);
-        } else {
-            float f = load1(src, sdt, i);
-            // truncation toward zero, as a C cast
-            if (ddt == I64) reinterpret_cast<int64_t*>(dst)[i] = (int64_t)f;
-            else reinterpret_cast<int32_t*>(dst)[i] = (int32_t)f;
+__device__ __forceinline__ float scalar_fn(float x, int op, float a, float b) {
+    if (op == MBRT_SCALAR_ADD) return x + a;
+    if (op == MBRT_SCALAR_MUL) return x * a;
+    return fminf(fmaxf(x, a), b);
+}
+
+__device__ __forceinline__ float unary_fn(float x, int op, float value) {
+    if (op == MBRT_UNARY_NEG) return -x;
+    return x > value ? 1.0f : 0.0f;
+}
+
+// In-place scalar ops (op code runs after the loads) and out-of-place unary ops.
+template <int DT, bool UNARY>
+__global__ __launch_bounds__(kThreads) void map_vec_kernel(const void* src, void* dst, int64_t n, int op, float a,
+                                                     float b) {
+    MBRT_FLAT_PROLOGUE(ve_for<DT>())
+    if (groups > 0) {
+        Vec<DT, VE> v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u].load(src, clamp_group(base + u * kThreads, groups) * VE);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t g = base + u * kThreads;
+            if (g < groups) {
+                float f[VE];
+                v[u].to_f32(f);
+#pragma unroll
+                for (int i = 0; i < VE; ++i) f[i] = UNARY ? unary_fn(f[i], op, a) : scalar_fn(f[i], op, a, b);
+                v[u].from_f32(f);
+                v[u].store(dst, g * VE);
+            }
+        }
+    }
+    if (blockIdx.x == 0) {
+        const int64_t e = groups * VE + threadIdx.x;
+        if (e < n) {
+            const float x = ld1<DT>(src, e);
+            st1<DT>(dst, e, UNARY ? unary_fn(x, op, a) : scalar_fn(x, op, a, b));
         }
     }
 }
 
-// ---- scalar / unary -----------------------------------------------------------------
+// ---- runtime-dtype element kernels (unaligned operands, integer conversions) ---------
 
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void scalar_kernel(void* data, int dt, int64_t n, int op, float a, float b) {
-    auto f1 = [&](float x) {
-        if (op == MBRT_SCALAR_ADD) return x + a;
-        if (op == MBRT_SCALAR_MUL) return x * a;
-        return fminf(fmaxf(x, a), b);
-    };
-    flat_loop<VEC>(
-        n,
-        [&](int64_t e) {
-            float f[8];
-            load8(data, dt, e, f);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) f[i] = f1(f[i]);
-            store8(data, dt, e, f);
-        },
-        [&](int64_t e) { store1(data, dt, e, f1(load1(data, dt, e))); });
+__global__ __launch_bounds__(kThreads) void convert_elem_kernel(const void* src, int sdt, void* dst, int ddt,
+                                                         int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i < n; i += (int64_t)gridDim.x * kThreads) {
+        if (sdt == I64 || sdt == I32) {
+            const int64_t v = sdt == I64 ? reinterpret_cast<const int64_t*>(src)[i]
+                                         : (int64_t)reinterpret_cast<const int32_t*>(src)[i];
+            if (ddt == I64) reinterpret_cast<int64_t*>(dst)[i] = v;
+            else if (ddt == I32) reinterpret_cast<int32_t*>(dst)[i] = (int32_t)v;
+            else store1(dst, ddt, i, (float)v);
+        } else {
+            const float f = load1(src, sdt, i);
+            // float -> int truncates toward zero, as a C cast
+            if (ddt == I64) reinterpret_cast<int64_t*>(dst)[i] = (int64_t)f;
+            else if (ddt == I32) reinterpret_cast<int32_t*>(dst)[i] = (int32_t)f;
+            else store1(dst, ddt, i, f);
+        }
+    }
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void unary_kernel(const void* src, void* dst, int dt, int64_t n, int op,
-                                                  float value) {
-    auto f1 = [&](float x) {
-        if (op == MBRT_UNARY_NEG) return -x;
-        return x > value ? 1.0f : 0.0f;
-    };
-    flat_loop<VEC>(
-        n,
-        [&](int64_t e) {
-            float f[8];
-            load8(src, dt, e, f);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) f[i] = f1(f[i]);
-            store8(dst, dt, e, f);
-        },
-        [&](int64_t e) { store1(dst, dt, e, f1(load1(src, dt, e))); });
+__global__ __launch_bounds__(kThreads) void map_elem_kernel(const void* src, void* dst, int dt, int64_t n, int op,
+                                                     float a, float b, int unary) {
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i < n; i += (int64_t)gridDim.x * kThreads) {
+        const float x = load1(src, dt, i);
+        store1(dst, dt, i, unary ? unary_fn(x, op, a) : scalar_fn(x, op, a, b));
+    }
 }
+
+inline dim3 elem_grid(int64_t n) { return dim3((unsigned)std::min<int64_t>(std::max<int64_t>(1, ceil_div(n, kThreads)), 1 << 20)); }
+inline dim3 vec_grid(int64_t n, int ve) { return dim3((unsigned)std::max<int64_t>(1, ceil_div(n / ve, (int64_t)kThreads * kU))); }
 
 // ---- binary -------------------------------------------------------------------------
 
@@ -174,19 +181,42 @@ __device__ __forceinline__ float binop(float x, float y) {
     return x / y;
 }
 
-template <int OP, bool VEC>
-__global__ __launch_bounds__(kThreads) void binary_kernel(const void* a, const void* b, void* out, int dt, int64_t n) {
-    flat_loop<VEC>(
-        n,
-        [&](int64_t e) {
-            float x[8], y[8];
-            load8(a, dt, e, x);
-            load8(b, dt, e, y);
+template <int OP, int DT>
+__global__ __launch_bounds__(kThreads) void binary_vec_kernel(const void* a, const void* b, void* out, int64_t n) {
+    MBRT_FLAT_PROLOGUE(ve_for<DT>())
+    if (groups > 0) {
+        Vec<DT, VE> va[kU], vb[kU];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) x[i] = binop<OP>(x[i], y[i]);
-            store8(out, dt, e, x);
-        },
-        [&](int64_t e) { store1(out, dt, e, binop<OP>(load1(a, dt, e), load1(b, dt, e))); });
+        for (int u = 0; u < kU; ++u) {
+            const int64_t g = clamp_group(base + u * kThreads, groups) * VE;
+            va[u].load(a, g);
+            vb[u].load(b, g);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t g = base + u * kThreads;
+            if (g < groups) {
+                float x[VE], y[VE];
+                va[u].to_f32(x);
+                vb[u].to_f32(y);
+#pragma unroll
+                for (int i = 0; i < VE; ++i) x[i] = binop<OP>(x[i], y[i]);
+                va[u].from_f32(x);
+                va[u].store(out, g * VE);
+            }
+        }
+    }
+    if (blockIdx.x == 0) {
+        const int64_t e = groups * VE + threadIdx.x;
+        if (e < n) st1<DT>(out, e, binop<OP>(ld1<DT>(a, e), ld1<DT>(b, e)));
+    }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kThreads) void binary_elem_kernel(const void* a, const void* b, void* out, int dt,
+                                                        int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    for (; i < n; i += (int64_t)gridDim.x * kThreads) store1(out, dt, i, binop<OP>(load1(a, dt, i), load1(b, dt, i)));
 }
 
 struct BcastArgs {
@@ -312,15 +342,16 @@ int mbrt_convert(const void* src, int src_dtype, void* dst, int dst_dtype, int64
     MBRT_REQUIRE(n >= 0, MBRT_E_SHAPE, "%s: negative size", op);
     if (n == 0) return MBRT_OK;
     hipStream_t st = as_stream(stream);
-    if (is_float_dt(src_dtype) && is_float_dt(dst_dtype)) {
-        const bool vec = vec_ok(src) && vec_ok(dst);
-        const dim3 grid((unsigned)flat_grid_for(vec, n));
-        if (vec) hipLaunchKernelGGL(convert_float_kernel<true>, grid, dim3(kThreads), 0, st, src, src_dtype, dst, dst_dtype, n);
-        else hipLaunchKernelGGL(convert_float_kernel<false>, grid, dim3(kThreads), 0, st, src, src_dtype, dst, dst_dtype, n);
+    if (is_float_dt(src_dtype) && is_float_dt(dst_dtype) && vec_ok(src) && vec_ok(dst)) {
+        const int ve = (src_dtype == F32 || dst_dtype == F32) ? 4 : 8;
+        with_dt(src_dtype, [&](auto sd) {
+            with_dt(dst_dtype, [&](auto dd) {
+                constexpr int S = decltype(sd)::value, D = decltype(dd)::value;
+                hipLaunchKernelGGL((convert_vec_kernel<S, D>), vec_grid(n, ve), dim3(kThreads), 0, st, src, dst, n);
+            });
+        });
     } else {
-        int64_t grid = std::min<int64_t>(ceil_div(n, kThreads), 1 << 20);
-        hipLaunchKernelGGL(convert_int_kernel, dim3((unsigned)grid), dim3(kThreads), 0, st, src, src_dtype, dst,
-                           dst_dtype, n);
+        hipLaunchKernelGGL(convert_elem_kernel, elem_grid(n), dim3(kThreads), 0, st, src, src_dtype, dst, dst_dtype, n);
     }
     return check_launch(op);
 }
@@ -331,10 +362,13 @@ int mbrt_scalar_op(void* data, int dtype, int64_t n, int op_code, float a, float
     MBRT_REQUIRE(op_code >= 0 && op_code <= 2, MBRT_E_INVALID_ARG, "%s: bad op %d", op, op_code);
     MBRT_REQUIRE(n >= 0, MBRT_E_SHAPE, "%s: negative size", op);
     if (n == 0) return MBRT_OK;
-    const bool vec = vec_ok(data);
-    const dim3 grid((unsigned)flat_grid_for(vec, n));
-    if (vec) hipLaunchKernelGGL(scalar_kernel<true>, grid, dim3(kThreads), 0, as_stream(stream), data, dtype, n, op_code, a, b);
-    else hipLaunchKernelGGL(scalar_kernel<false>, grid, dim3(kThreads), 0, as_stream(stream), data, dtype, n, op_code, a, b);
+    hipStream_t st = as_stream(stream);
+    if (vec_ok(data)) {
+        if (dtype == F32) hipLaunchKernelGGL((map_vec_kernel<F32, false>), vec_grid(n, 4), dim3(kThreads), 0, st, data, data, n, op_code, a, b);
+        else hipLaunchKernelGGL((map_vec_kernel<F16, false>), vec_grid(n, 8), dim3(kThreads), 0, st, data, data, n, op_code, a, b);
+    } else {
+        hipLaunchKernelGGL(map_elem_kernel, elem_grid(n), dim3(kThreads), 0, st, data, data, dtype, n, op_code, a, b, 0);
+    }
     return check_launch(op);
 }
 
@@ -344,10 +378,13 @@ int mbrt_unary(const void* src, void* dst, int dtype, int64_t n, int op_code, fl
     MBRT_REQUIRE(op_code == 0 || op_code == 1, MBRT_E_INVALID_ARG, "%s: bad op %d", op, op_code);
     MBRT_REQUIRE(n >= 0, MBRT_E_SHAPE, "%s: negative size", op);
     if (n == 0) return MBRT_OK;
-    const bool vec = vec_ok(src) && vec_ok(dst);
-    const dim3 grid((unsigned)flat_grid_for(vec, n));
-    if (vec) hipLaunchKernelGGL(unary_kernel<true>, grid, dim3(kThreads), 0, as_stream(stream), src, dst, dtype, n, op_code, value);
-    else hipLaunchKernelGGL(unary_kernel<false>, grid, dim3(kThreads), 0, as_stream(stream), src, dst, dtype, n, op_code, value);
+    hipStream_t st = as_stream(stream);
+    if (vec_ok(src) && vec_ok(dst)) {
+        if (dtype == F32) hipLaunchKernelGGL((map_vec_kernel<F32, true>), vec_grid(n, 4), dim3(kThreads), 0, st, src, dst, n, op_code, value, 0.0f);
+        else hipLaunchKernelGGL((map_vec_kernel<F16, true>), vec_grid(n, 8), dim3(kThreads), 0, st, src, dst, n, op_code, value, 0.0f);
+    } else {
+        hipLaunchKernelGGL(map_elem_kernel, elem_grid(n), dim3(kThreads), 0, st, src, dst, dtype, n, op_code, value, 0.0f, 1);
+    }
     return check_launch(op);
 }
 
@@ -362,9 +399,15 @@ int mbrt_binary(const void* a, const void* b, void* out, int dtype, int64_t n, i
     const bool vec = vec_ok(a) && vec_ok(b) && vec_ok(out);
     dispatch_op(op_code, [&](auto opc) {
         constexpr int OP = decltype(opc)::value;
-        const dim3 grid((unsigned)flat_grid_for(vec, n));
-        if (vec) hipLaunchKernelGGL((binary_kernel<OP, true>), grid, dim3(kThreads), 0, st, a, b, out, dtype, n);
-        else hipLaunchKernelGGL((binary_kernel<OP, false>), grid, dim3(kThreads), 0, st, a, b, out, dtype, n);
+        if (vec) {
+            with_dt(dtype, [&](auto dtc) {
+                constexpr int DT = decltype(dtc)::value;
+                hipLaunchKernelGGL((binary_vec_kernel<OP, DT>), vec_grid(n, ve_for<DT>()), dim3(kThreads), 0, st, a, b,
+                                   out, n);
+            });
+        } else {
+            hipLaunchKernelGGL(binary_elem_kernel<OP>, elem_grid(n), dim3(kThreads), 0, st, a, b, out, dtype, n);
+        }
     });
     return check_launch(op);
 }

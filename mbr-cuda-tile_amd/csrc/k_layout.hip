@@ -81,31 +81,28 @@ __global__ __launch_bounds__(kThreads) void row_copy_kernel(RowCopyArgs a) {
     const uint32_t base = blockIdx.x * (kThreads * U) + threadIdx.x;
     Word v[U];
     int64_t dst_off[U];
-    bool ok[U];
+    // all loads first (index clamped into the copy), then predicated stores
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        uint32_t i = base + u * kThreads;
-        ok[u] = i < a.total_vec;
-        if (ok[u]) {
-            uint32_t row, col;
-            fdivmod(i, a.vpr, row, col);
-            int64_t off = (int64_t)col * W;
-            dst_off[u] = (int64_t)row * a.dst_pitch + (int64_t)col * W;
+        const uint32_t i = min(base + u * kThreads, a.total_vec - 1);
+        uint32_t row, col;
+        fdivmod(i, a.vpr, row, col);
+        int64_t off = (int64_t)col * W;
+        dst_off[u] = (int64_t)row * a.dst_pitch + (int64_t)col * W;
 #pragma unroll
-            for (int d = 0; d < kMaxOuter; ++d) {
-                if (d < a.nd) {
-                    uint32_t q, r;
-                    fdivmod(row, a.outer[d], q, r);
-                    off += (int64_t)r * a.outer_stride[d];
-                    row = q;
-                }
+        for (int d = 0; d < kMaxOuter; ++d) {
+            if (d < a.nd) {
+                uint32_t q, r;
+                fdivmod(row, a.outer[d], q, r);
+                off += (int64_t)r * a.outer_stride[d];
+                row = q;
             }
-            v[u] = *reinterpret_cast<const Word*>(a.src + off);
         }
+        v[u] = *reinterpret_cast<const Word*>(a.src + off);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        if (ok[u]) *reinterpret_cast<Word*>(a.dst + dst_off[u]) = v[u];
+        if (base + u * kThreads < a.total_vec) *reinterpret_cast<Word*>(a.dst + dst_off[u]) = v[u];
     }
 }
 
@@ -163,7 +160,7 @@ int launch_row_copy(const char* src, char* dst, const Dims& dm, int esize, int64
             a.outer[d] = make_fastdiv((uint32_t)dm.shape[src_d]);
             a.outer_stride[d] = dm.stride[src_d] * esize;
         }
-        constexpr int U = 4;
+        constexpr int U = 2;
         int64_t grid = ceil_div(total, (int64_t)kThreads * U);
         hipLaunchKernelGGL((row_copy_kernel<W, U>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
     } else {

@@ -3,14 +3,17 @@
 //
 //   out[r, d] = x[r, d] * (1 / sqrt(sum_d x[r, d]^2 + eps)) * gamma[d] * scale
 //
-// Register-resident fast path: a group of G lanes (16/32/64) owns one row and holds it as
-// ceil(D / 8 / G) 8-element vectors per lane, so every byte of x is read from HBM once,
-// the sum of squares is a G-lane butterfly, and the output is written once.  The
-// reference launches one 1024-wide tile per row (62.5 % masked at D = 384) and, at
-// D != 256, runs the residual add as a separate pass.  At D = 384: 48 vectors per row,
-// G = 16 lanes x 3 vectors, 4 rows per wave, 16 rows per 256-thread block.
-// The fallback (unaligned pointers, D % 8 != 0 or D > 4096) is one wave per row with
-// a scalar two-pass loop.
+// Register-resident fast path: a group of G lanes (16/32/64) owns one row, split into
+// 16-byte chunks of VE elements (VE = 4 for f32 rows, 8 for bf16/f16 rows); lane l holds
+// chunks l, l+G, l+2G, ..., so each load instruction of the group reads G consecutive
+// 16-byte chunks.  Every byte of x (and of the residual) is read from HBM once, the sum
+// of squares is a G-lane butterfly, the sum (residual variant) and the output are written
+// once.  The reference launches one 1024-wide tile per row (62.5 % masked at D = 384) and,
+// at D != 256, runs the residual add as a separate pass.
+//   D = 384 f32 : 96 chunks -> G = 16 lanes x 6 chunks, 4 rows per wave
+//   D = 384 bf16: 48 chunks -> G = 16 lanes x 3 chunks
+// Fallback (unaligned pointers, D not a whole number of chunks, D > 4096): one wave per
+// row with a scalar two-pass loop.
 #include "abi_common.hpp"
 
 #include <algorithm>
@@ -29,48 +32,75 @@ struct RmsArgs {
     int xdt, gdt, sdt, odt;
     int64_t rows;
     int dim;
-    int nvec;  // dim / 8
+    int nchunk;  // dim / VE
     float scale;
     float eps;
 };
 
-template <int G, int NVMAX>
+// One block = 256 / G rows.  gamma * scale is staged once per block in LDS as f32.  The
+// row loads are unconditional (row and chunk indices clamped into the tensor), so all of a
+// lane's x (and residual) chunks are in flight together; stores are predicated.
+template <int XDT, int ODT, bool RES, int G, int NC>
 __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
-    constexpr int kRowsPerBlock = kThreads / G;
+    constexpr int VE = (XDT == F32 || ODT == F32) ? 4 : 8;
+    extern __shared__ float gs[];
     const int lane = threadIdx.x % G;
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / G;
+    const int64_t row = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
     const bool valid = row < a.rows;
-    const int64_t base = row * a.dim;
-
-    float v[NVMAX][8];
+    const int64_t base = (valid ? row : a.rows - 1) * a.dim;
+    const int lastc = a.nchunk - 1;
+    Vec<XDT, VE> xv[NC], rv[NC];
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+        const int c = min(lane + G * k, lastc);
+        xv[k].load(a.x, base + c * VE);
+        if (RES) rv[k].load(a.res, base + c * VE);
+    }
+    for (int d = threadIdx.x; d < a.dim; d += kThreads) gs[d] = load1(a.gamma, a.gdt, d) * a.scale;
+    float v[NC][VE];
     float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NVMAX; ++k) {
-        const int c = lane + G * k;
-        if (valid && c < a.nvec) {
-            load8(a.x, a.xdt, base + c * 8, v[k]);
-            if (a.res != nullptr) {
-                float r[8];
-                load8(a.res, a.xdt, base + c * 8, r);
+    for (int k = 0; k < NC; ++k) {
+        xv[k].to_f32(v[k]);
+        if (RES) {
+            float r[VE];
+            rv[k].to_f32(r);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[k][i] = round_through(v[k][i] + r[i], a.sdt);
-                if (a.sum_out != nullptr) store8(a.sum_out, a.sdt, base + c * 8, v[k]);
+            for (int i = 0; i < VE; ++i) v[k][i] = v[k][i] + r[i];
+            if (XDT != F32) {  // the sum is stored in the input dtype and normalised from there
+                Vec<XDT, VE> t;
+                t.from_f32(v[k]);
+                t.to_f32(v[k]);
             }
+        }
+        const bool in = lane + G * k <= lastc;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ss = fmaf(v[k][i], v[k][i], ss);
+        for (int i = 0; i < VE; ++i) ss = fmaf(v[k][i], in ? v[k][i] : 0.0f, ss);
+    }
+    const int full = a.nchunk / G;
+    if (RES && a.sum_out != nullptr && valid) {
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+            if (k < full || lane + G * k <= lastc) {
+                Vec<XDT, VE> t;
+                t.from_f32(v[k]);
+                t.store(a.sum_out, base + (lane + G * k) * VE);
+            }
         }
     }
     ss = group_sum<G>(ss);
-    const float inv = rsqrtf(ss + a.eps) * a.scale;
+    const float inv = rsqrtf(ss + a.eps);
+    __syncthreads();
+    if (!valid) return;
 #pragma unroll
-    for (int k = 0; k < NVMAX; ++k) {
-        const int c = lane + G * k;
-        if (valid && c < a.nvec) {
-            float g[8];
-            load8(a.gamma, a.gdt, c * 8, g);
+    for (int k = 0; k < NC; ++k) {
+        if (k < full || lane + G * k <= lastc) {
+            const int c = lane + G * k;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[k][i] = v[k][i] * inv * g[i];
-            store8(a.out, a.odt, base + c * 8, v[k]);
+            for (int i = 0; i < VE; ++i) v[k][i] = v[k][i] * inv * gs[c * VE + i];
+            Vec<ODT, VE> o;
+            o.from_f32(v[k]);
+            o.store(a.out, base + c * VE);
         }
     }
 }
@@ -106,26 +136,45 @@ __global__ __launch_bounds__(kThreads) void rms_loop_kernel(RmsArgs a) {
     }
 }
 
+template <int XDT, int ODT, bool RES, int G, int NC>
+void launch_fast(const RmsArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((rms_fast_kernel<XDT, ODT, RES, G, NC>), dim3((unsigned)ceil_div(a.rows, kThreads / G)),
+                       dim3(kThreads), a.dim * sizeof(float), st, a);
+}
+
+// Group width / chunks per lane for `nchunk` chunks; false when the row is too long.
+template <int XDT, int ODT, bool RES>
+bool launch_chunks(const RmsArgs& a, hipStream_t st) {
+    const int n = a.nchunk;
+    if (n <= 32) launch_fast<XDT, ODT, RES, 16, 2>(a, st);
+    else if (n <= 64) launch_fast<XDT, ODT, RES, 16, 4>(a, st);
+    else if (n <= 96) launch_fast<XDT, ODT, RES, 16, 6>(a, st);
+    else if (n <= 128) launch_fast<XDT, ODT, RES, 16, 8>(a, st);
+    else if (n <= 512) launch_fast<XDT, ODT, RES, 64, 8>(a, st);
+    else if (n <= 1024) launch_fast<XDT, ODT, RES, 64, 16>(a, st);
+    else return false;
+    return true;
+}
+
 int launch_rms(RmsArgs a, hipStream_t st, const char* op) {
     if (a.rows == 0) return MBRT_OK;
-    bool vec = (a.dim % 8) == 0 && a.dim <= 4096 && aligned(a.x, 16) && aligned(a.gamma, 16) &&
-               aligned(a.out, 16) && (a.res == nullptr || aligned(a.res, 16)) &&
-               (a.sum_out == nullptr || aligned(a.sum_out, 16));
-    if (vec) {
-        a.nvec = a.dim / 8;
-        int G;
-        int nv;
-        if (a.nvec <= 16 * 4) G = 16;
-        else if (a.nvec <= 32 * 4) G = 32;
-        else G = 64;
-        nv = (a.nvec + G - 1) / G;
-        const int rows_per_block = kThreads / G;
-        const dim3 grid((unsigned)ceil_div(a.rows, rows_per_block));
-        if (G == 16) hipLaunchKernelGGL((rms_fast_kernel<16, 4>), grid, dim3(kThreads), 0, st, a);
-        else if (G == 32) hipLaunchKernelGGL((rms_fast_kernel<32, 4>), grid, dim3(kThreads), 0, st, a);
-        else if (nv <= 4) hipLaunchKernelGGL((rms_fast_kernel<64, 4>), grid, dim3(kThreads), 0, st, a);
-        else hipLaunchKernelGGL((rms_fast_kernel<64, 8>), grid, dim3(kThreads), 0, st, a);
-    } else {
+    const int ve = (a.xdt == F32 || a.odt == F32) ? 4 : 8;
+    const bool res = a.res != nullptr;
+    const bool al = aligned(a.x, 16) && aligned(a.out, 16) && (!res || aligned(a.res, 16)) &&
+                    (a.sum_out == nullptr || aligned(a.sum_out, 16));
+    // the fused path stores the residual sum in the input dtype
+    const bool sum_ok = !res || a.sdt == a.xdt;
+    bool done = false;
+    if (al && sum_ok && a.dim % ve == 0 && (a.dim * dt_size(a.xdt)) % 16 == 0 && a.dim <= 4096) {
+        a.nchunk = a.dim / ve;
+        with_dt(a.xdt, [&](auto xt) {
+            with_dt(a.odt, [&](auto ot) {
+                constexpr int X = decltype(xt)::value, O = decltype(ot)::value;
+                done = res ? launch_chunks<X, O, true>(a, st) : launch_chunks<X, O, false>(a, st);
+            });
+        });
+    }
+    if (!done) {
         const dim3 grid((unsigned)ceil_div(a.rows, kThreads / 64));
         hipLaunchKernelGGL(rms_loop_kernel, grid, dim3(kThreads), 0, st, a);
     }

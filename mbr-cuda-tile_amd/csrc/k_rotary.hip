@@ -2,9 +2,9 @@
 // Interleaved pairs: for pair i of a head vector at position n,
 //   (x0, x1) -> (x0 c - x1 s, x0 s + x1 c),  c = cos[n, i], s = sin[n, i].
 //
-// In-place kernel: one thread rotates an 8-element (4-pair) group of q and the same group
-// of k, with one 16-byte load and store each (bf16) and the 4 matching cos/sin values
-// read from the [n_pos, D/2] tables, which stay L2-resident (801 x 32 x 4 B = 100 KB each)
+// In-place kernel: one thread rotates a VE-element group of q (VE = 8 for bf16/f16: one
+// 16-byte access; 4 for f32) and the same group of k, with the VE/2 matching cos/sin
+// values read from the [n_pos, D/2] tables, which stay L2-resident (801 x 32 x 4 B = 100 KB each)
 // while being broadcast over batch*heads.  The position of a row is row % n_pos for
 // [B*H, N, D] and (row / H) % n_pos for [B, N, H, D].
 #include "abi_common.hpp"
@@ -25,22 +25,27 @@ struct RotArgs {
     int64_t rows, n_pos, heads;
     int D;
     int layout;
-    uint32_t groups;   // rows * D / 8
-    FastDiv gpr;       // groups per row (D / 8)
+    uint32_t groups;   // rows * D / VE
+    FastDiv gpr;       // groups per row (D / VE)
     FastDiv npos_div;
     FastDiv heads_div;
 };
 
-__device__ __forceinline__ void rotate8(float (&x)[8], const float (&c)[4], const float (&s)[4]) {
+template <int VE>
+__device__ __forceinline__ void rotate(float (&x)[VE], const float (&c)[VE / 2], const float (&s)[VE / 2]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < VE / 2; ++i) {
         const float x0 = x[2 * i], x1 = x[2 * i + 1];
         x[2 * i] = x0 * c[i] - x1 * s[i];
         x[2 * i + 1] = x0 * s[i] + x1 * c[i];
     }
 }
 
+// One thread = one VE-element group (VE/2 pairs) of q and the same group of k.  All four
+// loads (q, k, cos, sin) are issued before the rotation.
+template <int DT, int TDT, bool HAS_K>
 __global__ __launch_bounds__(kThreads) void rotary_vec_kernel(RotArgs a) {
+    constexpr int VE = ve_for<DT>();
     const uint32_t g = blockIdx.x * kThreads + threadIdx.x;
     if (g >= a.groups) return;
     uint32_t row, c;
@@ -48,23 +53,26 @@ __global__ __launch_bounds__(kThreads) void rotary_vec_kernel(RotArgs a) {
     uint32_t pos_row = row;
     if (a.layout == MBRT_LAYOUT_BNHD) pos_row = fdiv(row, a.heads_div);
     const uint32_t n = pos_row - fdiv(pos_row, a.npos_div) * a.npos_div.d;
-    const int64_t t = (int64_t)n * (a.D / 2) + (int64_t)c * 4;
-    float cs[4], sn[4];
-    load4(a.cosp, a.tdt, t, cs);
-    load4(a.sinp, a.tdt, t, sn);
-    const int64_t e = (int64_t)g * 8;
-    float x[8];
-    load8(a.q, a.dt, e, x);
-    if (a.k != nullptr) {
-        float y[8];
-        load8(a.k, a.dt, e, y);
-        rotate8(x, cs, sn);
-        rotate8(y, cs, sn);
-        store8(a.q, a.dt, e, x);
-        store8(a.k, a.dt, e, y);
-    } else {
-        rotate8(x, cs, sn);
-        store8(a.q, a.dt, e, x);
+    const int64_t t = (int64_t)n * (a.D / 2) + (int64_t)c * (VE / 2);
+    const int64_t e = (int64_t)g * VE;
+    Vec<DT, VE> q, k;
+    Vec<TDT, VE / 2> cv, sv;
+    q.load(a.q, e);
+    if (HAS_K) k.load(a.k, e);
+    cv.load(a.cosp, t);
+    sv.load(a.sinp, t);
+    float cs[VE / 2], sn[VE / 2], x[VE];
+    cv.to_f32(cs);
+    sv.to_f32(sn);
+    q.to_f32(x);
+    rotate<VE>(x, cs, sn);
+    q.from_f32(x);
+    q.store(a.q, e);
+    if (HAS_K) {
+        k.to_f32(x);
+        rotate<VE>(x, cs, sn);
+        k.from_f32(x);
+        k.store(a.k, e);
     }
 }
 
@@ -101,35 +109,49 @@ struct SplitArgs {
     int64_t B, N, H, D, outN;
 };
 
-// One thread per 8-element group of the [B, H, outN, D] outputs (q, k and v together).
+// One thread per VE-element group of the [B, H, outN, D] outputs (q, k and v together);
+// the three qkv loads and the table loads are issued before any use.
+template <int IDT, int ODT, int TDT>
 __global__ __launch_bounds__(kThreads) void split_qkv_vec_kernel(SplitArgs a, uint32_t groups, FastDiv gpr,
                                                           FastDiv outn_div, FastDiv h_div) {
+    constexpr int VE = (IDT == F32 || ODT == F32) ? 4 : 8;
     const uint32_t g = blockIdx.x * kThreads + threadIdx.x;
     if (g >= groups) return;
     uint32_t orow, c, bh, n, b, h;
     fdivmod(g, gpr, orow, c);        // orow = (b*H + h)*outN + n
     fdivmod(orow, outn_div, bh, n);
     fdivmod(bh, h_div, b, h);
-    const int64_t e = (int64_t)g * 8;
-    float xq[8], xk[8], xv[8];
-    if ((int64_t)n < a.N) {
-        const int64_t src = ((int64_t)b * a.N + n) * (3 * a.H * a.D) + (int64_t)h * a.D + (int64_t)c * 8;
-        load8(a.qkv, a.idt, src, xq);
-        load8(a.qkv, a.idt, src + a.H * a.D, xk);
-        load8(a.qkv, a.idt, src + 2 * a.H * a.D, xv);
-        float cs[4], sn[4];
-        const int64_t t = (int64_t)n * (a.D / 2) + (int64_t)c * 4;
-        load4(a.cosp, a.tdt, t, cs);
-        load4(a.sinp, a.tdt, t, sn);
-        rotate8(xq, cs, sn);
-        rotate8(xk, cs, sn);
-    } else {
+    const int64_t e = (int64_t)g * VE;
+    const bool pad = (int64_t)n >= a.N;
+    const int64_t nn = pad ? a.N - 1 : n;  // padded rows load a valid row and store zeros
+    const int64_t src = ((int64_t)b * a.N + nn) * (3 * a.H * a.D) + (int64_t)h * a.D + (int64_t)c * VE;
+    const int64_t t = nn * (a.D / 2) + (int64_t)c * (VE / 2);
+    Vec<IDT, VE> vq, vk, vv;
+    Vec<TDT, VE / 2> cv, sv;
+    vq.load(a.qkv, src);
+    vk.load(a.qkv, src + a.H * a.D);
+    vv.load(a.qkv, src + 2 * a.H * a.D);
+    cv.load(a.cosp, t);
+    sv.load(a.sinp, t);
+    float xq[VE], xk[VE], xv[VE], cs[VE / 2], sn[VE / 2];
+    vq.to_f32(xq);
+    vk.to_f32(xk);
+    vv.to_f32(xv);
+    cv.to_f32(cs);
+    sv.to_f32(sn);
+    rotate<VE>(xq, cs, sn);
+    rotate<VE>(xk, cs, sn);
+    if (pad) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xq[i] = xk[i] = xv[i] = 0.0f;
+        for (int i = 0; i < VE; ++i) xq[i] = xk[i] = xv[i] = 0.0f;
     }
-    store8(a.q, a.odt, e, xq);
-    store8(a.k, a.odt, e, xk);
-    store8(a.v, a.odt, e, xv);
+    Vec<ODT, VE> o;
+    o.from_f32(xq);
+    o.store(a.q, e);
+    o.from_f32(xk);
+    o.store(a.k, e);
+    o.from_f32(xv);
+    o.store(a.v, e);
 }
 
 __global__ __launch_bounds__(kThreads) void split_qkv_scalar_kernel(SplitArgs a) {
@@ -198,17 +220,28 @@ int mbrt_rotary_inplace(void* q, void* k, int dtype, const void* cos_table, cons
     a.D = (int)dim_head;
     a.layout = layout;
     hipStream_t st = as_stream(stream);
-    const int64_t groups = rows * dim_head / 8;
-    const bool tab_al = trig_dtype == F32 ? (aligned(cos_table, 16) && aligned(sin_table, 16))
-                                          : (aligned(cos_table, 8) && aligned(sin_table, 8));
-    const bool vec = dim_head % 8 == 0 && aligned(q, 16) && (k == nullptr || aligned(k, 16)) && tab_al &&
+    const int ve = dtype == F32 ? 4 : 8;
+    const int64_t groups = rows * dim_head / ve;
+    const uintptr_t tab_bytes = (uintptr_t)(ve / 2) * dt_size(trig_dtype);  // table bytes per group
+    const bool tab_al = aligned(cos_table, tab_bytes) && aligned(sin_table, tab_bytes);
+    const bool vec = dim_head % ve == 0 && aligned(q, 16) && (k == nullptr || aligned(k, 16)) && tab_al &&
                      groups < (1ll << 32) && rows < (1ll << 31);
     if (vec) {
         a.groups = (uint32_t)groups;
-        a.gpr = make_fastdiv((uint32_t)(dim_head / 8));
+        a.gpr = make_fastdiv((uint32_t)(dim_head / ve));
         a.npos_div = make_fastdiv((uint32_t)n_pos);
         a.heads_div = make_fastdiv((uint32_t)heads);
-        hipLaunchKernelGGL(rotary_vec_kernel, dim3((unsigned)ceil_div(groups, kThreads)), dim3(kThreads), 0, st, a);
+        const dim3 grid((unsigned)ceil_div(groups, kThreads));
+        with_dt(dtype, [&](auto dt_) {
+            constexpr int DTv = decltype(dt_)::value;
+            if (k != nullptr) {
+                if (trig_dtype == F32) hipLaunchKernelGGL((rotary_vec_kernel<DTv, F32, true>), grid, dim3(kThreads), 0, st, a);
+                else hipLaunchKernelGGL((rotary_vec_kernel<DTv, BF16, true>), grid, dim3(kThreads), 0, st, a);
+            } else {
+                if (trig_dtype == F32) hipLaunchKernelGGL((rotary_vec_kernel<DTv, F32, false>), grid, dim3(kThreads), 0, st, a);
+                else hipLaunchKernelGGL((rotary_vec_kernel<DTv, BF16, false>), grid, dim3(kThreads), 0, st, a);
+            }
+        });
     } else {
         const int64_t pairs = rows * dim_head / 2;
         hipLaunchKernelGGL(rotary_scalar_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(pairs, kThreads), 1 << 20)),
@@ -246,15 +279,27 @@ int mbrt_split_qkv_heads_rotary(const void* qkv, int qkv_dtype, const void* cos_
     a.D = D;
     a.outN = out_N;
     hipStream_t st = as_stream(stream);
-    const int64_t groups = total / 8;
-    const bool tab_al = trig_dtype == F32 ? (aligned(cos_table, 16) && aligned(sin_table, 16))
-                                          : (aligned(cos_table, 8) && aligned(sin_table, 8));
-    const bool vec = D % 8 == 0 && aligned(qkv, 16) && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && tab_al &&
-                     groups < (1ll << 32);
+    const int ve = (qkv_dtype == F32 || out_dtype == F32) ? 4 : 8;
+    const int64_t groups = total / ve;
+    const uintptr_t tab_bytes = (uintptr_t)(ve / 2) * dt_size(trig_dtype);
+    const bool tab_al = aligned(cos_table, tab_bytes) && aligned(sin_table, tab_bytes);
+    const bool vec = D % ve == 0 && N >= 1 && aligned(qkv, 16) && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
+                     tab_al && groups < (1ll << 32);
     if (vec) {
-        hipLaunchKernelGGL(split_qkv_vec_kernel, dim3((unsigned)ceil_div(groups, kThreads)), dim3(kThreads), 0, st, a,
-                           (uint32_t)groups, make_fastdiv((uint32_t)(D / 8)), make_fastdiv((uint32_t)out_N),
-                           make_fastdiv((uint32_t)H));
+        const dim3 grid((unsigned)ceil_div(groups, kThreads));
+        const FastDiv gpr = make_fastdiv((uint32_t)(D / ve)), od = make_fastdiv((uint32_t)out_N),
+                      hd = make_fastdiv((uint32_t)H);
+        with_dt(qkv_dtype, [&](auto it) {
+            with_dt(out_dtype, [&](auto ot) {
+                constexpr int IDTv = decltype(it)::value, ODTv = decltype(ot)::value;
+                if (trig_dtype == F32)
+                    hipLaunchKernelGGL((split_qkv_vec_kernel<IDTv, ODTv, F32>), grid, dim3(kThreads), 0, st, a,
+                                       (uint32_t)groups, gpr, od, hd);
+                else
+                    hipLaunchKernelGGL((split_qkv_vec_kernel<IDTv, ODTv, BF16>), grid, dim3(kThreads), 0, st, a,
+                                       (uint32_t)groups, gpr, od, hd);
+            });
+        });
     } else {
         const int64_t pairs = total / 2;
         hipLaunchKernelGGL(split_qkv_scalar_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(pairs, kThreads), 1 << 20)),

@@ -1,19 +1,15 @@
 // Row softmax with f32 accumulation (the scale_softmax* family, src/mbr_cuda_tile.cu:5092-5285):
 //   z = scale * x;  p = exp(z - max z) / sum exp(z - max z)   per row of `cols` elements.
 //
-// A group of G lanes owns a row and keeps it in registers, so the input is read once and
-// the output written once (the reference uses one 2048-wide tile per row: 61 % of the
-// lanes idle at 801 columns, 97 % at 60).  Rows of 801 / 60 elements do not start on
-// 16-byte boundaries, so the group walks the 16-byte-aligned vectors that cover its row
-// (measured from the buffer base, which must be 16-byte aligned): interior vectors are
-// loaded and stored whole, the two edge vectors element-wise with masking.  Neighbouring
-// rows share an edge vector; each group writes only its own elements, so in-place
-// (out == in) is safe.
-//   801 cols f32 : 202 vectors/row -> G = 64, 4 vectors per lane
-//   801 cols bf16: 102 vectors/row -> G = 64, 2 vectors per lane
-//   60 cols f32  : <= 16 vectors   -> G = 16, 1 vector per lane, 16 rows per block
-//   60 cols bf16 : <= 9 vectors    -> G = 16, 1 vector per lane
-// Rows too long for registers (> 64 lanes x 16 vectors) use a three-pass loop kernel.
+// A group of G lanes owns one row and keeps it in registers: lane l holds elements
+// l, l+G, l+2G, ...  Every load and store instruction of the group then touches G
+// consecutive elements (256 B per wave instruction for f32 rows at G = 64), rows need
+// no alignment (801-element rows start at arbitrary offsets), and only the last slot
+// of a row is predicated.  The row is read once and written once.  exp is evaluated as
+// exp2 of the pre-scaled input (z * log2 e), one v_exp_f32 per element.
+//   801 cols : G = 64, 13 elements per lane, 4 rows per 256-thread block
+//   60 cols  : G = 16, 4 elements per lane, 16 rows per block
+// Rows longer than 64 x 32 elements use a three-pass loop kernel.
 #include "abi_common.hpp"
 
 #include <algorithm>
@@ -23,114 +19,55 @@ namespace mbrt {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr float kLog2e = 1.44269504088896340736f;
 
 struct SmArgs {
     const void* in;
     void* out;
     int odt;
     int64_t rows;
-    int64_t cols;
-    int64_t total;  // rows * cols (elements in the buffer)
-    float scale;
+    int cols;
+    float scale_log2e;
 };
 
-template <int IDT>
-__device__ __forceinline__ void load_vec(const void* p, int64_t e, float* f) {
-    if (IDT == F32) {
-        float t[4];
-        load4(p, F32, e, t);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = t[i];
-    } else {
-        float t[8];
-        load8(p, IDT, e, t);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = t[i];
-    }
-}
-
-template <int IDT>
-__device__ __forceinline__ void store_vec(void* p, int odt, int64_t e, const float* f) {
-    if (IDT == F32) {
-        float t[4] = {f[0], f[1], f[2], f[3]};
-        store4(p, odt, e, t);
-    } else {
-        float t[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = f[i];
-        store8(p, odt, e, t);
-    }
-}
-
-template <int IDT, int G, int NV>
-__global__ __launch_bounds__(kThreads) void softmax_fast_kernel(SmArgs a) {
-    constexpr int VE = IDT == F32 ? 4 : 8;  // elements per 16-byte vector
+// Loads are unconditional (the row index and the element index are clamped into the
+// tensor), so all NM loads of a lane are issued before the first use; only stores are
+// predicated, and only the last slot of a row ever needs a per-lane predicate.
+template <int IDT, int G, int NM>
+__global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
     const int lane = threadIdx.x % G;
     const int64_t row = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
     const bool valid = row < a.rows;
-    const int64_t start = row * a.cols;
-    const int64_t end = start + a.cols;
-    const int64_t v0 = start / VE;
-
-    float x[NV][VE];
-    float m = -FLT_MAX;
+    const int64_t base = (valid ? row : a.rows - 1) * a.cols;
+    const int last = a.cols - 1;
+    float z[NM];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int64_t e0 = (v0 + lane + (int64_t)G * k) * VE;
-        const bool any = valid && e0 < end;
-        if (any && e0 >= start && e0 + VE <= end) {  // interior vector
-            load_vec<IDT>(a.in, e0, x[k]);
+    for (int k = 0; k < NM; ++k) z[k] = ld1<IDT>(a.in, base + min(lane + G * k, last));
+    float m = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < VE; ++i) {
-                x[k][i] *= a.scale;
-                m = fmaxf(m, x[k][i]);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < VE; ++i) {
-                const int64_t e = e0 + i;
-                float v = -FLT_MAX;
-                if (any && e >= start && e < end) {
-                    v = load1(a.in, IDT, e) * a.scale;
-                    m = fmaxf(m, v);
-                }
-                x[k][i] = v;
-            }
-        }
+    for (int k = 0; k < NM; ++k) {
+        z[k] = lane + G * k <= last ? z[k] * a.scale_log2e : -INFINITY;
+        m = fmaxf(m, z[k]);
     }
     m = group_max<G>(m);
     float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int64_t e0 = (v0 + lane + (int64_t)G * k) * VE;
-        const bool interior = valid && e0 >= start && e0 + VE <= end;
-#pragma unroll
-        for (int i = 0; i < VE; ++i) {
-            const int64_t e = e0 + i;
-            float p = fast_exp(x[k][i] - m);
-            if (!interior && !(valid && e >= start && e < end)) p = 0.0f;
-            x[k][i] = p;
-            s += p;
-        }
+    for (int k = 0; k < NM; ++k) {
+        z[k] = __builtin_amdgcn_exp2f(z[k] - m);  // masked slots: exp2(-inf) = 0
+        s += z[k];
     }
     s = group_sum<G>(s);
     const float inv = 1.0f / s;
+    const int full = a.cols / G;  // slots [0, full) hold a valid element in every lane
+    auto store_all = [&](auto odt_tag) {
+        constexpr int ODT = decltype(odt_tag)::value;
+        if (!valid) return;
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int64_t e0 = (v0 + lane + (int64_t)G * k) * VE;
-        const bool any = valid && e0 < end;
-#pragma unroll
-        for (int i = 0; i < VE; ++i) x[k][i] *= inv;
-        if (any && e0 >= start && e0 + VE <= end) {
-            store_vec<IDT>(a.out, a.odt, e0, x[k]);
-        } else if (any) {
-#pragma unroll
-            for (int i = 0; i < VE; ++i) {
-                const int64_t e = e0 + i;
-                if (e >= start && e < end) store1(a.out, a.odt, e, x[k][i]);
-            }
+        for (int k = 0; k < NM; ++k) {
+            if (k < full || lane + G * k <= last) st1<ODT>(a.out, base + lane + G * k, z[k] * inv);
         }
-    }
+    };
+    with_dt(a.odt, store_all);
 }
 
 // Long rows: one wave per row, three passes (max, sum, write) over global memory.
@@ -139,40 +76,41 @@ __global__ __launch_bounds__(kThreads) void softmax_loop_kernel(SmArgs a, int id
     const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
     if (row >= a.rows) return;
     const int64_t start = row * a.cols;
-    float m = -FLT_MAX;
-    for (int64_t c = lane; c < a.cols; c += 64) m = fmaxf(m, load1(a.in, idt, start + c) * a.scale);
+    float m = -INFINITY;
+    for (int64_t c = lane; c < a.cols; c += 64) m = fmaxf(m, load1(a.in, idt, start + c) * a.scale_log2e);
     m = group_max<64>(m);
     float s = 0.0f;
-    for (int64_t c = lane; c < a.cols; c += 64) s += fast_exp(load1(a.in, idt, start + c) * a.scale - m);
+    for (int64_t c = lane; c < a.cols; c += 64)
+        s += __builtin_amdgcn_exp2f(load1(a.in, idt, start + c) * a.scale_log2e - m);
     s = group_sum<64>(s);
     const float inv = 1.0f / s;
     for (int64_t c = lane; c < a.cols; c += 64)
-        store1(a.out, a.odt, start + c, fast_exp(load1(a.in, idt, start + c) * a.scale - m) * inv);
+        store1(a.out, a.odt, start + c,
+               __builtin_amdgcn_exp2f(load1(a.in, idt, start + c) * a.scale_log2e - m) * inv);
 }
 
+template <int IDT, int G, int NM>
+void launch_rows(const SmArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL((softmax_rows_kernel<IDT, G, NM>), dim3((unsigned)ceil_div(a.rows, kThreads / G)),
+                       dim3(kThreads), 0, st, a);
+}
+
+// Picks the group width and slots per lane for a row length; false when too long.
 template <int IDT>
 bool launch_fast(const SmArgs& a, hipStream_t st) {
-    constexpr int VE = IDT == F32 ? 4 : 8;
-    // vectors a row can touch: ceil(cols / VE) + 1 (misaligned start)
-    const int64_t nvec = (a.cols + VE - 1) / VE + 1;
-    auto grid = [&](int G) { return dim3((unsigned)ceil_div(a.rows, kThreads / G)); };
-    if (nvec <= 16) {
-        hipLaunchKernelGGL((softmax_fast_kernel<IDT, 16, 1>), grid(16), dim3(kThreads), 0, st, a);
-    } else if (nvec <= 32) {
-        hipLaunchKernelGGL((softmax_fast_kernel<IDT, 32, 1>), grid(32), dim3(kThreads), 0, st, a);
-    } else if (nvec <= 64) {
-        hipLaunchKernelGGL((softmax_fast_kernel<IDT, 64, 1>), grid(64), dim3(kThreads), 0, st, a);
-    } else if (nvec <= 128) {
-        hipLaunchKernelGGL((softmax_fast_kernel<IDT, 64, 2>), grid(64), dim3(kThreads), 0, st, a);
-    } else if (nvec <= 256) {
-        hipLaunchKernelGGL((softmax_fast_kernel<IDT, 64, 4>), grid(64), dim3(kThreads), 0, st, a);
-    } else if (nvec <= 512) {
-        hipLaunchKernelGGL((softmax_fast_kernel<IDT, 64, 8>), grid(64), dim3(kThreads), 0, st, a);
-    } else if (nvec <= 1024) {
-        hipLaunchKernelGGL((softmax_fast_kernel<IDT, 64, 16>), grid(64), dim3(kThreads), 0, st, a);
-    } else {
-        return false;
-    }
+    const int c = a.cols;
+    if (c <= 8) launch_rows<IDT, 8, 1>(a, st);
+    else if (c <= 16) launch_rows<IDT, 16, 1>(a, st);
+    else if (c <= 32) launch_rows<IDT, 16, 2>(a, st);
+    else if (c <= 64) launch_rows<IDT, 16, 4>(a, st);
+    else if (c <= 128) launch_rows<IDT, 32, 4>(a, st);
+    else if (c <= 256) launch_rows<IDT, 64, 4>(a, st);
+    else if (c <= 512) launch_rows<IDT, 64, 8>(a, st);
+    else if (c <= 832) launch_rows<IDT, 64, 13>(a, st);
+    else if (c <= 1024) launch_rows<IDT, 64, 16>(a, st);
+    else if (c <= 1344) launch_rows<IDT, 64, 21>(a, st);
+    else if (c <= 2048) launch_rows<IDT, 64, 32>(a, st);
+    else return false;
     return true;
 }
 
@@ -188,7 +126,7 @@ int mbrt_softmax_rows(const void* in, int in_dtype, void* out, int out_dtype, in
     const char* op = "mbrt_softmax_rows";
     MBRT_REQUIRE_FLOAT_DT(in_dtype, op);
     MBRT_REQUIRE_FLOAT_DT(out_dtype, op);
-    MBRT_REQUIRE(rows >= 0 && cols >= 1, MBRT_E_SHAPE, "%s: bad shape", op);
+    MBRT_REQUIRE(rows >= 0 && cols >= 1 && cols < (1 << 30), MBRT_E_SHAPE, "%s: bad shape", op);
     if (rows == 0) return MBRT_OK;
     MBRT_REQUIRE(in && out, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
     MBRT_REQUIRE(in != out || in_dtype == out_dtype, MBRT_E_INVALID_ARG, "%s: in-place needs equal dtypes", op);
@@ -197,17 +135,13 @@ int mbrt_softmax_rows(const void* in, int in_dtype, void* out, int out_dtype, in
     a.out = out;
     a.odt = out_dtype;
     a.rows = rows;
-    a.cols = cols;
-    a.total = rows * cols;
-    a.scale = scale;
+    a.cols = (int)cols;
+    a.scale_log2e = scale * kLog2e;
     hipStream_t st = as_stream(stream);
-    bool done = false;
-    // the vector path walks vectors aligned to the buffer base: both bases 16B-aligned
-    if (aligned(in, 16) && aligned(out, 16)) {
-        if (in_dtype == F32) done = launch_fast<F32>(a, st);
-        else if (in_dtype == BF16) done = launch_fast<BF16>(a, st);
-        else done = launch_fast<F16>(a, st);
-    }
+    bool done;
+    if (in_dtype == F32) done = launch_fast<F32>(a, st);
+    else if (in_dtype == BF16) done = launch_fast<BF16>(a, st);
+    else done = launch_fast<F16>(a, st);
     if (!done) {
         hipLaunchKernelGGL(softmax_loop_kernel, dim3((unsigned)ceil_div(rows, kThreads / 64)), dim3(kThreads), 0, st, a,
                            in_dtype);

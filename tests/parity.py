@@ -2,7 +2,9 @@
 
 * Integer / byte / index work and pure copies: bit-exact.
 * f32 outputs: max_i |y_i - yhat_i| / max(|yhat_i|, tau) <= 1e-5, tau = 1e-3 * RMS(yhat),
-  where yhat is the oracle's double-precision value rounded once to f32.
+  where yhat is the oracle's double-precision value rounded once to f32.  For outputs
+  that are sums or differences of products (rotary pairs, complex mask products,
+  reductions) the denominator also includes the magnitude of those terms (`den`).
 * bf16 / f16 outputs: one correct rounding alone can move a value by 2^-8 (bf16), which
   exceeds 2e-3, so the rule compares against yhat = the double-precision value rounded
   once to the output format: |y_i - yhat_i| <= 1 ulp(max(|yhat_i|, tau)) elementwise,
@@ -76,8 +78,16 @@ def _ulp(x: np.ndarray, dt: int) -> np.ndarray:
     return np.exp2(e - (p - 1))
 
 
-def assert_close(y: np.ndarray, yhat: np.ndarray, dt: int, what: str = "", rtol: float | None = None) -> dict:
-    """Apply the rule for output dtype `dt` (F32 / BF16 / F16); returns the measured errors."""
+def assert_close(y: np.ndarray, yhat: np.ndarray, dt: int, what: str = "", rtol: float | None = None,
+                 den: np.ndarray | None = None) -> dict:
+    """Apply the rule for output dtype `dt` (F32 / BF16 / F16); returns the measured errors.
+
+    `den` (f32 rule only): per-element magnitude of the terms that the exact result is
+    a sum or difference of, for ops whose outputs cancel (rotations, complex products,
+    reductions).  The f32 error is then measured relative to max(|yhat|, den, tau): an
+    f32 evaluation of a - b carries ~2^-24 (|a| + |b|) absolute error however small
+    a - b is, in the reference's kernels as in these.
+    """
     assert y.shape == yhat.shape, f"{what}: shape {y.shape} != {yhat.shape}"
     a, b = _f32(y, dt), _f32(yhat, dt)
     ok = _check_specials(a, b, what)
@@ -87,7 +97,9 @@ def assert_close(y: np.ndarray, yhat: np.ndarray, dt: int, what: str = "", rtol:
     tau = TAU_REL * float(np.sqrt(np.mean(b * b)))
     if dt == F32:
         tol = RTOL_F32 if rtol is None else rtol
-        den = np.maximum(np.abs(b), tau if tau > 0 else 1e-30)
+        den = np.maximum(np.abs(b), tau if tau > 0 else 1e-30) if den is None else \
+            np.maximum(np.maximum(np.abs(b), np.asarray(den, np.float64).reshape(-1)[ok.reshape(-1)].reshape(b.shape)),
+                       tau if tau > 0 else 1e-30)
         err = np.abs(a - b) / den
         worst = int(np.argmax(err))
         assert err[worst] <= tol, (f"{what}: f32 max rel err {err[worst]:.3e} > {tol:.0e} at {worst}: "
@@ -105,3 +117,27 @@ def assert_close(y: np.ndarray, yhat: np.ndarray, dt: int, what: str = "", rtol:
     if dt != F32:
         assert norm <= NORM_RTOL_LOWP, f"{what}: norm-wise rel err {norm:.3e} > {NORM_RTOL_LOWP}"
     return {"max_rel": elem, "norm_rel": norm}
+
+
+def pair_den(x: np.ndarray) -> np.ndarray:
+    """Per-element |(x0, x1)| of interleaved pairs (last dim), for rotations."""
+    x = np.asarray(x, np.float64)
+    pr = x.reshape(x.shape[:-1] + (x.shape[-1] // 2, 2))
+    n = np.sqrt((pr * pr).sum(-1, keepdims=True))
+    return np.broadcast_to(n, pr.shape).reshape(x.shape)
+
+
+def merge_den(orc, stft, masks, mb, B, F, T, C):
+    """sum_e |stft| |mask_e| / count for every complex output of the band merge (f32),
+    repeated for the re and im parts: the magnitude its f32 products cancel from."""
+    s_abs = np.zeros_like(stft)
+    s_abs[..., 0] = np.hypot(stft[..., 0], stft[..., 1])
+    m_abs = []
+    for m in masks:
+        m = np.asarray(m, np.float32).reshape(B, T, -1, 2)
+        a = np.zeros_like(m)
+        a[..., 0] = np.hypot(m[..., 0], m[..., 1])
+        m_abs.append(a)
+    cnt = mb["bands_per_freq"].astype(np.float32)
+    out = orc.band_mask_merge(s_abs, m_abs, F32, mb["csr_offsets"], mb["csr_indices"], cnt, F32, F32, B, F, T, C)
+    return np.repeat(out[..., :1], 2, axis=-1)

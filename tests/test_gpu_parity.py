@@ -14,9 +14,8 @@ import pytest
 import torch
 
 import mbrt
-import oracle as O
 from gpu_util import empty, say, to_dev, to_host
-from parity import BF16, F16, F32, I32, I64, assert_bitexact, assert_close
+from parity import BF16, F16, F32, I32, I64, assert_bitexact, assert_close, merge_den, pair_den
 
 pytestmark = pytest.mark.gpu
 
@@ -208,7 +207,7 @@ def test_reductions(orc, dev):
         out = empty(shape[:-1], F32)
         mbrt.reduce_last(to_dev(x, F32), out, mbrt.REDUCE_SUM)
         torch.cuda.synchronize()
-        assert_close(to_host(out, F32), orc.reduce_last(x, 0), F32, "sum last", rtol=1e-5)
+        assert_close(to_host(out, F32), orc.reduce_last(x, 0), F32, "sum last", den=np.abs(x).sum(-1))
         mbrt.reduce_last(to_dev(x, F32), out, mbrt.REDUCE_MAX)
         torch.cuda.synchronize()
         assert_bitexact(to_host(out, F32), x.max(-1), "max last")
@@ -414,7 +413,7 @@ def test_rotary_variants(orc, dev, layout, dt, tdt, D):
     mbrt.rotary_(qd, None, to_dev(cos, tdt), to_dev(sin, tdt), layout, heads=H)
     torch.cuda.synchronize()
     rq, _ = orc.rotary(q, None, dt, cos, sin, tdt, N, H, layout=layout)
-    assert_close(to_host(qd, dt), rq, dt, "rotary")
+    assert_close(to_host(qd, dt), rq, dt, "rotary", den=pair_den(orc.to_f32(q, dt)))
 
 
 @pytest.mark.parametrize("N,out_n,idt,odt", [(60, 64, BF16, BF16), (801, 801, BF16, BF16), (17, 17, F32, F32),
@@ -430,8 +429,8 @@ def test_split_qkv_rotary(orc, dev, N, out_n, idt, odt):
     mbrt.split_qkv_rotary(to_dev(qkv, idt), to_dev(cos, F32), to_dev(sin, F32), q, k, v, H)
     torch.cuda.synchronize()
     rq, rk, rv = orc.split_qkv(qkv, idt, cos, sin, F32, odt, B, N, H, D, out_n)
-    assert_close(to_host(q, odt), rq, odt, "q")
-    assert_close(to_host(k, odt), rk, odt, "k")
+    assert_close(to_host(q, odt), rq, odt, "q", den=pair_den(orc.to_f32(rq, odt)))
+    assert_close(to_host(k, odt), rk, odt, "k", den=pair_den(orc.to_f32(rk, odt)))
     assert_bitexact(to_host(v, odt), rv, "v")
 
 
@@ -470,7 +469,8 @@ def test_band_merge_bl5b_full(orc, dev):
     torch.cuda.synchronize()
     ref = orc.band_mask_merge(stft, [mask.reshape(B, T, J, 2)], F32, mb["csr_offsets"], mb["csr_indices"], cnt, F32, F32,
                               B, F, T, 2)
-    print("BL-5b errors", assert_close(to_host(out, F32), ref, F32, "merge"))
+    den = merge_den(orc, stft, [mask], mb, B, F, T, 2)
+    print("BL-5b errors", assert_close(to_host(out, F32), ref, F32, "merge", den=den))
     # gather then merge with mask 1+0j is the identity on every bin (bit-exact, counts 1 and 2)
     g = empty((B, T, J * 2), F32)
     mbrt.band_gather(sd, to_dev(mb["freq_indices"], I32), g)
@@ -499,7 +499,8 @@ def test_band_merge_variants(orc, dev, mdt, cdt, odt, S, idt):
     torch.cuda.synchronize()
     ref = orc.band_mask_merge(stft, [m.reshape(B, T, J, 2) for m in masks], mdt, mb["csr_offsets"], mb["csr_indices"],
                               cnt, cdt, odt, B, F, T, 2)
-    assert_close(to_host(out, odt), ref, odt, "merge")
+    den = merge_den(orc, stft, [orc.to_f32(m, mdt) for m in masks], mb, B, F, T, 2) if odt == F32 else None
+    assert_close(to_host(out, odt), ref, odt, "merge", den=den)
 
 
 def test_band_merge_many_bands_per_freq(orc, dev):
@@ -522,7 +523,8 @@ def test_band_merge_many_bands_per_freq(orc, dev):
                          out, C)
     torch.cuda.synchronize()
     ref = orc.band_mask_merge(stft, [mask.reshape(B, T, J, 2)], F32, off, ind, cnt, F32, F32, B, F, T, C)
-    assert_close(to_host(out, F32), ref, F32, "merge chunked")
+    mbd = dict(bands_per_freq=cnt.astype(np.int32), csr_offsets=off, csr_indices=ind)
+    assert_close(to_host(out, F32), ref, F32, "merge chunked", den=merge_den(orc, stft, [mask], mbd, B, F, T, C))
 
 
 def test_zero_dc(orc, dev):
