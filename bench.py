@@ -1,7 +1,7 @@
 """Benchmark of the MelBandRoformer tensor-op hot path on one MI355X.
 
-One step = one pass of every BASELINE op at its full chunk shape (BL-1 .. BL-5), each
-on synthetic inputs already resident in HBM:
+One step = one pass of every op of the MelBandRoformer tensor path at its full chunk
+shape (BL-1 .. BL-5), each on synthetic inputs already resident in HBM:
   BL-1  residual add + RMSNorm f32 [48060, 384] (writes the sum and the normed rows)
   BL-2  GELU bf16 [48060, 1536]; GLU bf16 [48060, 3072]; sigmoid gate x head merge bf16
         attn [60, 8, 801, 64] + logits [48060, 8]
@@ -11,7 +11,8 @@ on synthetic inputs already resident in HBM:
   BL-5  band gather and mask merge, batch 4, 60 mel bands (3958 stereo band-bins)
 value = sum of algorithmic bytes / sum of op times (GB/s, all ops); per-op GB/s and the
 fraction of the 8 TB/s HBM peak are in config.per_op.  Op times are HIP events recorded
-on the stream the kernels run on.  Each op cycles through enough buffer sets that the
+on the stream the kernels run on.  The K steps are timed op-major: each op's K calls run
+back to back, so every op pays for its own cache write-backs.  Each op cycles through enough buffer sets that the
 working set between two uses of a set exceeds 1 GB, so the 256 MB MALL cannot serve
 repeats.  Algorithmic bytes count every input read once and every output written once.
 
@@ -48,6 +49,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=None)
+    ap.add_argument("--only", default=None,
+                    help="comma-separated op-name substrings: time only those ops (tuning runs; "
+                         "value then covers the selected ops only)")
     return ap.parse_args()
 
 
@@ -260,6 +264,9 @@ def main():
     torch.cuda.set_device(0)
     bands = band_tables(torch, mbrt)
     ops = build_ops(torch, mbrt, bands)
+    if args.only:
+        keys = [k for k in args.only.split(",") if k]
+        ops = [op for op in ops if any(k in op.name for k in keys)]
     for op in ops:
         first = op.make()
         ws = sum(t.numel() * t.element_size() for t in first.values())
@@ -268,30 +275,32 @@ def main():
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
 
-    def step(i, record):
-        evs = []
-        for op in ops:
-            b = op.sets[i % len(op.sets)]
-            if record:
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                op.run(b)
-                e1.record(stream)
-                evs.append((op, e0, e1))
-            else:
-                op.run(b)
-        return evs
+    # Op-major order: every op runs its K calls back to back (each call bracketed by HIP
+    # events on the stream the kernels run on), so an op's time includes the write-back of
+    # the dirty lines its own previous call left in the MALL, not those of a different op.
+    def run_op(op, i, record):
+        b = op.sets[i % len(op.sets)]
+        if not record:
+            op.run(b)
+            return None
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        op.run(b)
+        e1.record(stream)
+        return e0, e1
 
-    for i in range(args.warmup):
-        step(i, False)
+    for op in ops:
+        for i in range(args.warmup):
+            run_op(op, i, False)
     torch.cuda.synchronize()
     all_evs = []
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        all_evs += step(i, True)
+    for op in ops:
+        for i in range(args.steps):
+            all_evs.append((op, run_op(op, args.warmup + i, True)))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    for op, e0, e1 in all_evs:
+    for op, (e0, e1) in all_evs:
         op.times_ms.append(e0.elapsed_time(e1))
 
     per_op = {}

@@ -4,7 +4,11 @@ Outputs (git-ignored, shipped with the source tree):
   mbr-cuda-tile_amd/lib/libmbrt.so        C-ABI + HIP kernels (include/mbrt.h)
   mbr-cuda-tile_amd/lib/libmbrt_tensor.so C++ Tensor / tensor_tile:: / mbr_tile:: layer
 
-Usage: python mbr-cuda-tile_amd/build.py [-j N] [-v]
+Usage: python mbr-cuda-tile_amd/build.py [-j N] [-v] [-D NAME=VALUE ...] [--out DIR]
+
+-D passes a preprocessor definition to every HIP translation unit (the kernels' launch
+shapes can be overridden this way); --out puts objects and libraries under DIR instead of
+the package tree, so that such variants never replace the in-tree build.
 """
 from __future__ import annotations
 
@@ -76,43 +80,48 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out)
 
 
-def _compile(src: Path, obj: Path, verbose: bool) -> Path:
+def _compile(src: Path, obj: Path, defines: list[str], verbose: bool) -> Path:
     lang = ["-x", "hip"] if src.suffix in (".hip", ".cpp") else []
-    _run([HIPCC, *COMMON, *lang, "-c", str(src), "-o", str(obj)], verbose)
+    _run([HIPCC, *COMMON, *[f"-D{d}" for d in defines], *lang, "-c", str(src), "-o", str(obj)], verbose)
     return obj
 
 
-def _objects(srcdir: Path, names: list[str], tag: str, jobs: int, verbose: bool) -> list[Path]:
-    BUILD.mkdir(parents=True, exist_ok=True)
+def _objects(srcdir: Path, names: list[str], tag: str, build_dir: Path, defines: list[str], jobs: int,
+             verbose: bool) -> list[Path]:
+    build_dir.mkdir(parents=True, exist_ok=True)
     objs = []
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = []
         for n in names:
             src = srcdir / n
-            obj = BUILD / f"{tag}_{Path(n).stem}.o"
-            futs.append(ex.submit(_compile, src, obj, verbose))
+            obj = build_dir / f"{tag}_{Path(n).stem}.o"
+            futs.append(ex.submit(_compile, src, obj, defines, verbose))
         for f in futs:
             objs.append(f.result())
     return objs
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> dict[str, Path]:
+def build(jobs: int | None = None, verbose: bool = False, defines: list[str] | None = None,
+          out_dir: Path | str | None = None) -> dict[str, Path]:
     """Compile every source and link both libraries; returns their paths."""
     jobs = jobs or min(8, os.cpu_count() or 4)
-    LIB.mkdir(parents=True, exist_ok=True)
-    kobjs = _objects(CSRC, KERNEL_SOURCES, "k", jobs, verbose)
-    libmbrt = LIB / "libmbrt.so"
+    defines = list(defines or [])
+    lib_dir = Path(out_dir) if out_dir else LIB
+    build_dir = lib_dir / "_build" if out_dir else BUILD
+    lib_dir.mkdir(parents=True, exist_ok=True)
+    kobjs = _objects(CSRC, KERNEL_SOURCES, "k", build_dir, defines, jobs, verbose)
+    libmbrt = lib_dir / "libmbrt.so"
     tmp = libmbrt.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, kobjs)], verbose)
     os.replace(tmp, libmbrt)
     out = {"libmbrt": libmbrt}
     tsrc = [n for n in TENSOR_SOURCES if (HOST / n).exists()]
     if tsrc:
-        tobjs = _objects(HOST, tsrc, "t", jobs, verbose)
-        libt = LIB / "libmbrt_tensor.so"
+        tobjs = _objects(HOST, tsrc, "t", build_dir, defines, jobs, verbose)
+        libt = lib_dir / "libmbrt_tensor.so"
         tmp = libt.with_suffix(".so.tmp")
         _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, tobjs),
-              f"-L{LIB}", "-lmbrt", "-Wl,-rpath,$ORIGIN"], verbose)
+              f"-L{lib_dir}", "-lmbrt", "-Wl,-rpath,$ORIGIN"], verbose)
         os.replace(tmp, libt)
         out["libmbrt_tensor"] = libt
     return out
@@ -122,8 +131,10 @@ def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
     ap.add_argument("-v", action="store_true")
+    ap.add_argument("-D", dest="defines", action="append", default=[], metavar="NAME=VALUE")
+    ap.add_argument("--out", default=None, help="output directory (default: the package's lib/)")
     a = ap.parse_args(argv)
-    paths = build(a.j, a.v)
+    paths = build(a.j, a.v, a.defines, a.out)
     for k, p in paths.items():
         print(f"{k}: {p}")
     return 0

@@ -11,6 +11,7 @@
 
 #include "../../include/mbrt.h"
 #include "device.hpp"
+#include "tuning.hpp"
 
 namespace mbrt {
 

@@ -243,6 +243,19 @@ __device__ __forceinline__ float group_max(float v) {
 // one 8/16-byte (or two 16-byte) global access without touching the values, so a kernel
 // can issue every load before its first use; to_f32/from_f32 convert afterwards.
 
+// Non-temporal global accesses for data a kernel touches exactly once.  Kernels pick a
+// policy per operand: bit 0 of an NT argument marks loads non-temporal, bit 1 stores.
+template <int NT, class T>
+__device__ __forceinline__ T gld(const T* p) {
+    if constexpr ((NT & 1) != 0) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <int NT, class T>
+__device__ __forceinline__ void gst(T* p, T v) {
+    if constexpr ((NT & 2) != 0) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
 template <int DT>
 struct DtSize {
     static constexpr int value = DT == F32 ? 4 : 2;
@@ -254,32 +267,34 @@ struct Vec {
     static constexpr int kWords = kBytes / 4;
     uint32_t w[kWords];
 
+    template <int NT = 0>
     __device__ __forceinline__ void load(const void* p, int64_t e) {
         const char* b = reinterpret_cast<const char*>(p) + e * DtSize<DT>::value;
         static_assert(kBytes == 4 || kBytes == 8 || kBytes % 16 == 0, "Vec: unsupported width");
         if constexpr (kBytes == 4) {
-            w[0] = *reinterpret_cast<const uint32_t*>(b);
+            w[0] = gld<NT>(reinterpret_cast<const uint32_t*>(b));
         } else if constexpr (kBytes == 8) {
-            const u32x2 t = *reinterpret_cast<const u32x2*>(b);
+            const u32x2 t = gld<NT>(reinterpret_cast<const u32x2*>(b));
             w[0] = t.x; w[1] = t.y;
         } else {
 #pragma unroll
             for (int q = 0; q < kBytes / 16; ++q) {
-                const u32x4 t = reinterpret_cast<const u32x4*>(b)[q];
+                const u32x4 t = gld<NT>(reinterpret_cast<const u32x4*>(b) + q);
                 w[4 * q] = t.x; w[4 * q + 1] = t.y; w[4 * q + 2] = t.z; w[4 * q + 3] = t.w;
             }
         }
     }
+    template <int NT = 0>
     __device__ __forceinline__ void store(void* p, int64_t e) const {
         char* b = reinterpret_cast<char*>(p) + e * DtSize<DT>::value;
         if constexpr (kBytes == 4) {
-            *reinterpret_cast<uint32_t*>(b) = w[0];
+            gst<NT>(reinterpret_cast<uint32_t*>(b), w[0]);
         } else if constexpr (kBytes == 8) {
-            *reinterpret_cast<u32x2*>(b) = u32x2{w[0], w[1]};
+            gst<NT>(reinterpret_cast<u32x2*>(b), u32x2{w[0], w[1]});
         } else {
 #pragma unroll
             for (int q = 0; q < kBytes / 16; ++q)
-                reinterpret_cast<u32x4*>(b)[q] = u32x4{w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]};
+                gst<NT>(reinterpret_cast<u32x4*>(b) + q, u32x4{w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]});
         }
     }
     __device__ __forceinline__ void to_f32(float (&f)[VE]) const {
@@ -307,19 +322,19 @@ struct Vec {
     }
 };
 
-template <int DT>
+template <int DT, int NT = 0>
 __device__ __forceinline__ float ld1(const void* p, int64_t i) {
-    if constexpr (DT == F32) return reinterpret_cast<const float*>(p)[i];
-    const uint32_t h = reinterpret_cast<const uint16_t*>(p)[i];
+    if constexpr (DT == F32) return gld<NT>(reinterpret_cast<const float*>(p) + i);
+    const uint32_t h = gld<NT>(reinterpret_cast<const uint16_t*>(p) + i);
     if constexpr (DT == BF16) return __uint_as_float(h << 16);
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-template <int DT>
+template <int DT, int NT = 0>
 __device__ __forceinline__ void st1(void* p, int64_t i, float v) {
-    if constexpr (DT == F32) reinterpret_cast<float*>(p)[i] = v;
-    else if constexpr (DT == BF16) reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
-    else reinterpret_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v);
+    if constexpr (DT == F32) gst<NT>(reinterpret_cast<float*>(p) + i, v);
+    else if constexpr (DT == BF16) gst<NT>(reinterpret_cast<uint16_t*>(p) + i, f32_to_bf16_bits(v));
+    else gst<NT>(reinterpret_cast<uint16_t*>(p) + i, f32_to_f16_bits(v));
 }
 
 // Runs f(std::integral_constant<int, DT>) for a float dtype code known at run time.

@@ -18,7 +18,7 @@ namespace mbrt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kU = 2;        // groups per thread
+constexpr int kU = MBRT_ACT_U;  // groups per thread
 constexpr int kNoBias = -1;  // bias dtype tag: no bias
 
 __device__ __forceinline__ int64_t clamp_group(int64_t g, int64_t groups) { return g < groups ? g : groups - 1; }
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kThreads) void bias_act_vec_kernel(BiasActArgs a) {
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int64_t e = clamp_group(base + u * kThreads, groups) * VE;
-            xv[u].load(a.x, e);
+            xv[u].template load<MBRT_NT_ACT>(a.x, e);
             if constexpr (BDT != kNoBias) {
                 const uint32_t col = (uint32_t)e - fdiv((uint32_t)e, a.cols_div) * a.cols_div.d;
                 bv[u].load(a.bias, col);
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void bias_act_vec_kernel(BiasActArgs a) {
                 for (int i = 0; i < VE; ++i) v[i] = act_fn<LOWP>(v[i], a.act);
                 Vec<ODT, VE> o;
                 o.from_f32(v);
-                o.store(a.out, g * VE);
+                o.template store<MBRT_NT_ACT>(a.out, g * VE);
             }
         }
     }
@@ -122,8 +122,8 @@ __global__ __launch_bounds__(kThreads) void glu_vec_kernel(GluArgs a) {
         uint32_t row, c;
         fdivmod((uint32_t)clamp_group(base + u * kThreads, a.groups), a.gpr, row, c);
         const int64_t in0 = (int64_t)row * (2 * a.half) + (int64_t)c * VE;
-        xv[u].load(a.x, in0);
-        gv[u].load(a.x, in0 + a.half);
+        xv[u].template load<MBRT_NT_GLU>(a.x, in0);
+        gv[u].template load<MBRT_NT_GLU>(a.x, in0 + a.half);
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(kThreads) void glu_vec_kernel(GluArgs a) {
             for (int i = 0; i < VE; ++i) v[i] = v[i] * sigmoidf(gt[i]);
             Vec<ODT, VE> o;
             o.from_f32(v);
-            o.store(a.out, g * VE);
+            o.template store<MBRT_NT_GLU>(a.out, g * VE);
         }
     }
 }
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
         } else {
             src = (int64_t)g * VE;
         }
-        av[u].load(a.attn, src);
+        av[u].template load<MBRT_NT_GATE>(a.attn, src);
         gl[u] = ld1<GDT>(a.gate, (int64_t)token * a.H + h);
     }
 #pragma unroll
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
             for (int i = 0; i < VE; ++i) v[i] *= gv;
             Vec<ODT, VE> o;
             o.from_f32(v);
-            o.store(a.out, g * VE);
+            o.template store<MBRT_NT_GATE>(a.out, g * VE);
         }
     }
 }

@@ -37,6 +37,12 @@ __device__ __forceinline__ int64_t load_index(const void* p, int i64, int64_t i)
     return i64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
 }
 
+template <bool I64>
+__device__ __forceinline__ int ld_idx(const void* p, int64_t i) {
+    if constexpr (I64) return (int)reinterpret_cast<const int64_t*>(p)[i];
+    else return reinterpret_cast<const int32_t*>(p)[i];
+}
+
 struct GatherArgs {
     const float* stft;
     const void* idx;
@@ -50,15 +56,17 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 
 template <int ODT>
 __device__ __forceinline__ void store_complex(void* out, int64_t o, f32x2 v) {
-    if constexpr (ODT == F32) reinterpret_cast<f32x2*>(out)[o] = v;
-    else if constexpr (ODT == BF16) reinterpret_cast<uint32_t*>(out)[o] = pack_bf16x2(v.x, v.y);
-    else reinterpret_cast<uint32_t*>(out)[o] = pack_f16x2(v.x, v.y);
+    constexpr int NT = MBRT_NT_BAND;
+    if constexpr (ODT == F32) gst<NT>(reinterpret_cast<f32x2*>(out) + o, v);
+    else if constexpr (ODT == BF16) gst<NT>(reinterpret_cast<uint32_t*>(out) + o, pack_bf16x2(v.x, v.y));
+    else gst<NT>(reinterpret_cast<uint32_t*>(out) + o, pack_f16x2(v.x, v.y));
 }
 
 template <int MDT>
 __device__ __forceinline__ f32x2 load_complex(const void* p, int64_t i) {
-    if constexpr (MDT == F32) return reinterpret_cast<const f32x2*>(p)[i];
-    const uint32_t w = reinterpret_cast<const uint32_t*>(p)[i];
+    constexpr int NT = MBRT_NT_BAND;
+    if constexpr (MDT == F32) return gld<NT>(reinterpret_cast<const f32x2*>(p) + i);
+    const uint32_t w = gld<NT>(reinterpret_cast<const uint32_t*>(p) + i);
     if constexpr (MDT == BF16) return f32x2{bf16_lo(w), bf16_hi(w)};
     else return unpack_f16x2(w);
 }
@@ -67,7 +75,7 @@ __device__ __forceinline__ f32x2 load_complex(const void* p, int64_t i) {
 // of stft row idx[j0+jj] (512 contiguous bytes).  The row index is loaded once per lane and
 // broadcast with readlane; indices are clamped into the tensors so the 16 loads of a lane
 // are unconditional and in flight together.
-template <int ODT>
+template <int ODT, bool I64>
 __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
     __shared__ f32x2 tile[kTJ][kTT + 1];
     const int64_t j0 = (int64_t)blockIdx.x * kTJ;
@@ -75,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
     const int64_t b = blockIdx.z;
     const int lane = threadIdx.x % 64;
     const int w = wave_id();
-    const int f_lane = (int)load_index(a.idx, a.idx64, min(j0 + lane, a.J - 1));
+    const int f_lane = ld_idx<I64>(a.idx, min(j0 + lane, a.J - 1));
     const int64_t tq = min(t0 + lane, a.T - 1);
     const f32x2* stft = reinterpret_cast<const f32x2*>(a.stft) + b * a.F * a.T + tq;
     constexpr int kR = kTJ / (kThreads / 64);  // 16 rows per wave
@@ -83,7 +91,7 @@ __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
         const int64_t f = __builtin_amdgcn_readlane(f_lane, w + 4 * r);
-        v[r] = stft[f * a.T];
+        v[r] = gld<MBRT_NT_BAND>(stft + f * a.T);
     }
 #pragma unroll
     for (int r = 0; r < kR; ++r) tile[w + 4 * r][lane] = v[r];
@@ -101,66 +109,68 @@ __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
 struct MergeArgs {
     const float* stft;
     const void* mask[2];
-    int mdt;
-    int S;
     const void* off;
     const void* ind;
-    int idx64;
     const void* cnt;
-    int cdt;
     void* out;
-    int odt;
-    int64_t F, T, J, C;
+    int cdt;
+    int S;
+    int F, T, J;
+    FastDiv C;  // audio channels: freq = bin * C + ch
 };
 
 // Block (t-tile, f-tile, b*S+s).  Wave w owns freqs f0+w, f0+w+4, ... (8 of them) and lane
-// t of the tile: its stft values and CSR ranges are loaded up front.  The CSR entries of
-// the tile's freqs are staged 64 at a time: lane e loads mask[b, t, ind[c0+e]] for 16
-// frames, the tile is transposed through LDS, and each thread sums its freqs' entries in
-// ascending order.  All loads use clamped indices and are unconditional.
-template <int MDT, int ODT>
+// t of the tile.  Lane l of every wave holds off[f0+l] (l <= 32) and 1/count[f0+l]; the
+// ranges and scales of a wave's freqs are broadcast from there with readlane.  The CSR
+// entries of the tile's freqs are staged 64 at a time: lane e loads mask[b, t, ind[c0+e]]
+// for 16 frames, the tile is transposed through LDS, and each thread sums its freqs'
+// entries in ascending order.  All loads use clamped indices and are unconditional.
+template <int MDT, int ODT, bool I64>
 __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     __shared__ f32x2 ms[kME][kTT + 1];
-    const int64_t t0 = (int64_t)blockIdx.x * kTT;
-    const int64_t f0 = (int64_t)blockIdx.y * kTF;
-    const int64_t bs = blockIdx.z;  // b * S + s
-    const int64_t b = bs / a.S, s = bs - b * a.S;
-    const void* mask = a.mask[s];
+    const int t0 = blockIdx.x * kTT;
+    const int f0 = blockIdx.y * kTF;
+    const int bs = blockIdx.z;  // b * S + s
+    const int b = a.S == 2 ? bs >> 1 : bs;
+    const void* mask = a.mask[bs - b * a.S];
     const int lane = threadIdx.x % 64;
     const int w = wave_id();
     constexpr int kPer = kTF / (kThreads / 64);  // freqs per wave (8)
     constexpr int kR = kTT / (kThreads / 64);    // staged frames per wave (16)
-    const int64_t t = t0 + lane;
-    const int64_t tq = min(t, a.T - 1);
+    const int nf = min(kTF, a.F - f0);           // freqs in this tile
+    const int t = t0 + lane;
+    const int tq = min(t, a.T - 1);
 
-    const int64_t f_end = min(f0 + kTF, a.F);
-    const int64_t e_begin = load_index(a.off, a.idx64, f0);
-    const int64_t e_end = load_index(a.off, a.idx64, f_end);
+    const int off_lane = ld_idx<I64>(a.off, f0 + min(lane, nf));
+    float c = load1(a.cnt, a.cdt, f0 + min(lane, nf - 1));
+    const float inv_lane = 1.0f / (c > 1.0e-8f ? c : 1.0e-8f);
+    const int e_begin = __builtin_amdgcn_readlane(off_lane, 0);
+    const int e_end = __builtin_amdgcn_readlane(off_lane, nf);
 
+    const f32x2* srow = reinterpret_cast<const f32x2*>(a.stft) + ((int64_t)b * a.F + f0) * a.T + tq;
     f32x2 sv[kPer], acc[kPer];
-    int64_t eb[kPer], ee[kPer];
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
-        const int64_t f = min(f0 + w + 4 * r, a.F - 1);
-        eb[r] = load_index(a.off, a.idx64, f);
-        ee[r] = load_index(a.off, a.idx64, f + 1);
-        sv[r] = reinterpret_cast<const f32x2*>(a.stft)[(b * a.F + f) * a.T + tq];
+        sv[r] = gld<MBRT_NT_BAND>(srow + (int64_t)min(w + 4 * r, nf - 1) * a.T);
         acc[r] = f32x2{0.0f, 0.0f};
     }
-    for (int64_t c0 = e_begin; c0 < e_end; c0 += kME) {
-        const int64_t c1 = min(c0 + kME, e_end);
-        const int64_t j = load_index(a.ind, a.idx64, min(c0 + lane, c1 - 1));
+    const int64_t mbase = (int64_t)b * a.T;
+    for (int c0 = e_begin; c0 < e_end; c0 += kME) {
+        const int c1 = min(c0 + kME, e_end);
+        const int j = min(max(ld_idx<I64>(a.ind, min(c0 + lane, c1 - 1)), 0), a.J - 1);
         f32x2 mv[kR];
 #pragma unroll
-        for (int r = 0; r < kR; ++r) mv[r] = load_complex<MDT>(mask, (b * a.T + min(t0 + w + 4 * r, a.T - 1)) * a.J + j);
+        for (int r = 0; r < kR; ++r)
+            mv[r] = load_complex<MDT>(mask, (mbase + min(t0 + w + 4 * r, a.T - 1)) * a.J + j);
 #pragma unroll
         for (int r = 0; r < kR; ++r) ms[lane][w + 4 * r] = mv[r];
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
-            if (f0 + w + 4 * r >= a.F) continue;
-            const int64_t lo = max(eb[r], c0), hi = min(ee[r], c1);
-            for (int64_t e = lo; e < hi; ++e) {
+            const int fl = w + 4 * r;  // local freq (wave-uniform); entries [off[f], off[f+1])
+            const int lo = max(__builtin_amdgcn_readlane(off_lane, fl), c0);
+            const int hi = fl < nf ? min(__builtin_amdgcn_readlane(off_lane, fl + 1), c1) : lo;
+            for (int e = lo; e < hi; ++e) {
                 const f32x2 m = ms[e - c0][lane];
                 acc[r].x += sv[r].x * m.x - sv[r].y * m.y;
                 acc[r].y += sv[r].x * m.y + sv[r].y * m.x;
@@ -168,18 +178,22 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
         }
         __syncthreads();
     }
+    // readlane reads lanes regardless of EXEC: broadcast the scales while all lanes are active
+    float inv[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r)
+        inv[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_lane), w + 4 * r));
     if (t >= a.T) return;
-    const int64_t bins = a.F / a.C;
+    const int64_t bins = a.F / a.C.d;
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
-        const int64_t f = f0 + w + 4 * r;
-        if (f >= a.F) continue;
-        float den = load1(a.cnt, a.cdt, f);
-        den = den > 1.0e-8f ? den : 1.0e-8f;
-        const float inv = 1.0f / den;
-        const int64_t bin = f / a.C, ch = f - bin * a.C;
-        const int64_t o = (((b * a.S + s) * a.C + ch) * bins + bin) * a.T + t;
-        store_complex<ODT>(a.out, o, f32x2{acc[r].x * inv, acc[r].y * inv});
+        const int fl = w + 4 * r;
+        if (fl < nf) {
+            uint32_t bin, ch;
+            fdivmod((uint32_t)(f0 + fl), a.C, bin, ch);
+            const int64_t o = (((int64_t)bs * a.C.d + ch) * bins + bin) * a.T + t;
+            store_complex<ODT>(a.out, o, f32x2{acc[r].x * inv[r], acc[r].y * inv[r]});
+        }
     }
 }
 
@@ -216,7 +230,9 @@ int mbrt_band_gather(const float* stft, const void* freq_indices, int index_dtyp
     GatherArgs a{stft, freq_indices, index_dtype == I64, out, out_dtype, total_freq, frames, n_band_freqs};
     const dim3 grid((unsigned)ceil_div(n_band_freqs, kTJ), (unsigned)ceil_div(frames, kTT), (unsigned)B);
     with_dt(out_dtype, [&](auto ot) {
-        hipLaunchKernelGGL(band_gather_kernel<decltype(ot)::value>, grid, dim3(kThreads), 0, as_stream(stream), a);
+        constexpr int O = decltype(ot)::value;
+        if (index_dtype == I64) hipLaunchKernelGGL((band_gather_kernel<O, true>), grid, dim3(kThreads), 0, as_stream(stream), a);
+        else hipLaunchKernelGGL((band_gather_kernel<O, false>), grid, dim3(kThreads), 0, as_stream(stream), a);
     });
     return check_launch(op);
 }
@@ -239,28 +255,30 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
                  MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
     for (int s = 0; s < num_stems; ++s) MBRT_REQUIRE(masks[s] != nullptr, MBRT_E_INVALID_ARG, "%s: NULL mask", op);
     MBRT_REQUIRE(B * num_stems <= 65535, MBRT_E_SHAPE, "%s: batch*stems exceeds 65535", op);
+    MBRT_REQUIRE(total_freq < (1 << 30) && frames < (1 << 30) && n_band_freqs < (1 << 30) && B * frames < (1 << 30),
+                 MBRT_E_SHAPE, "%s: dimension exceeds 2^30", op);
     MergeArgs a{};
     a.stft = stft;
     a.mask[0] = masks[0];
     a.mask[1] = num_stems == 2 ? masks[1] : masks[0];
-    a.mdt = mask_dtype;
-    a.S = num_stems;
     a.off = csr_offsets;
     a.ind = csr_indices;
-    a.idx64 = index_dtype == I64;
     a.cnt = counts;
-    a.cdt = counts_dtype;
     a.out = out;
-    a.odt = out_dtype;
-    a.F = total_freq;
-    a.T = frames;
-    a.J = n_band_freqs;
-    a.C = channels;
+    a.cdt = counts_dtype;
+    a.S = num_stems;
+    a.F = (int)total_freq;
+    a.T = (int)frames;
+    a.J = (int)std::max<int64_t>(n_band_freqs, 1);
+    a.C = make_fastdiv((uint32_t)channels);
     const dim3 grid((unsigned)ceil_div(frames, kTT), (unsigned)ceil_div(total_freq, kTF), (unsigned)(B * num_stems));
     with_dt(mask_dtype, [&](auto mt) {
         with_dt(out_dtype, [&](auto ot) {
-            hipLaunchKernelGGL((band_merge_kernel<decltype(mt)::value, decltype(ot)::value>), grid, dim3(kThreads), 0,
-                               as_stream(stream), a);
+            constexpr int M = decltype(mt)::value, O = decltype(ot)::value;
+            if (index_dtype == I64)
+                hipLaunchKernelGGL((band_merge_kernel<M, O, true>), grid, dim3(kThreads), 0, as_stream(stream), a);
+            else
+                hipLaunchKernelGGL((band_merge_kernel<M, O, false>), grid, dim3(kThreads), 0, as_stream(stream), a);
         });
     });
     return check_launch(op);

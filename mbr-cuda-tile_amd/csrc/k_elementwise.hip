@@ -18,7 +18,7 @@ namespace mbrt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kU = 4;  // 8-element groups per thread
+constexpr int kU = MBRT_EW_U;  // 16-byte groups per thread
 
 // ---- fill / arange ------------------------------------------------------------------
 
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kThreads) void convert_vec_kernel(const void* src, 
     if (groups > 0) {
         Vec<SDT, VE> v[kU];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) v[u].load(src, clamp_group(base + u * kThreads, groups) * VE);
+        for (int u = 0; u < kU; ++u) v[u].template load<MBRT_NT_EW>(src, clamp_group(base + u * kThreads, groups) * VE);
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int64_t g = base + u * kThreads;
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void convert_vec_kernel(const void* src, 
                 v[u].to_f32(f);
                 Vec<DDT, VE> o;
                 o.from_f32(f);
-                o.store(dst, g * VE);
+                o.template store<MBRT_NT_EW>(dst, g * VE);
             }
         }
     }
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void map_vec_kernel(const void* src, void
     if (groups > 0) {
         Vec<DT, VE> v[kU];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) v[u].load(src, clamp_group(base + u * kThreads, groups) * VE);
+        for (int u = 0; u < kU; ++u) v[u].template load<MBRT_NT_EW>(src, clamp_group(base + u * kThreads, groups) * VE);
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int64_t g = base + u * kThreads;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kThreads) void map_vec_kernel(const void* src, void
 #pragma unroll
                 for (int i = 0; i < VE; ++i) f[i] = UNARY ? unary_fn(f[i], op, a) : scalar_fn(f[i], op, a, b);
                 v[u].from_f32(f);
-                v[u].store(dst, g * VE);
+                v[u].template store<MBRT_NT_EW>(dst, g * VE);
             }
         }
     }
@@ -189,8 +189,8 @@ __global__ __launch_bounds__(kThreads) void binary_vec_kernel(const void* a, con
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int64_t g = clamp_group(base + u * kThreads, groups) * VE;
-            va[u].load(a, g);
-            vb[u].load(b, g);
+            va[u].template load<MBRT_NT_EW>(a, g);
+            vb[u].template load<MBRT_NT_EW>(b, g);
         }
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void binary_vec_kernel(const void* a, con
 #pragma unroll
                 for (int i = 0; i < VE; ++i) x[i] = binop<OP>(x[i], y[i]);
                 va[u].from_f32(x);
-                va[u].store(out, g * VE);
+                va[u].template store<MBRT_NT_EW>(out, g * VE);
             }
         }
     }

@@ -98,11 +98,11 @@ __global__ __launch_bounds__(kThreads) void row_copy_kernel(RowCopyArgs a) {
                 row = q;
             }
         }
-        v[u] = *reinterpret_cast<const Word*>(a.src + off);
+        v[u] = gld<MBRT_NT_ROW>(reinterpret_cast<const Word*>(a.src + off));
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        if (base + u * kThreads < a.total_vec) *reinterpret_cast<Word*>(a.dst + dst_off[u]) = v[u];
+        if (base + u * kThreads < a.total_vec) gst<MBRT_NT_ROW>(reinterpret_cast<Word*>(a.dst + dst_off[u]), v[u]);
     }
 }
 
@@ -160,7 +160,7 @@ int launch_row_copy(const char* src, char* dst, const Dims& dm, int esize, int64
             a.outer[d] = make_fastdiv((uint32_t)dm.shape[src_d]);
             a.outer_stride[d] = dm.stride[src_d] * esize;
         }
-        constexpr int U = 2;
+        constexpr int U = MBRT_ROW_U;
         int64_t grid = ceil_div(total, (int64_t)kThreads * U);
         hipLaunchKernelGGL((row_copy_kernel<W, U>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
     } else {
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(TransposeArgs a) {
     for (int r = grp; r < kTile; r += kThreads / kTile) {
         int64_t p = p0 + lane, q = q0 + r;
         if (p < a.P && q < a.Q) {
-            tile[r][lane] = reinterpret_cast<const Elem*>(a.src)[src_base + q * a.sq + p];
+            tile[r][lane] = gld<MBRT_NT_TR>(reinterpret_cast<const Elem*>(a.src) + src_base + q * a.sq + p);
         }
     }
     __syncthreads();
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(TransposeArgs a) {
     for (int r = grp; r < kTile; r += kThreads / kTile) {
         int64_t p = p0 + r, q = q0 + lane;
         if (p < a.P && q < a.Q) {
-            reinterpret_cast<Elem*>(a.dst)[dst_base + p * a.out_p_pitch + q] = tile[lane][r];
+            gst<MBRT_NT_TR>(reinterpret_cast<Elem*>(a.dst) + dst_base + p * a.out_p_pitch + q, tile[lane][r]);
         }
     }
 }

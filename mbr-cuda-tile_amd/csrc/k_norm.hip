@@ -23,6 +23,7 @@ namespace {
 
 constexpr int kThreads = 256;
 
+
 struct RmsArgs {
     const void* x;
     const void* res;  // NULL: plain RMSNorm
@@ -53,8 +54,8 @@ __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
         const int c = min(lane + G * k, lastc);
-        xv[k].load(a.x, base + c * VE);
-        if (RES) rv[k].load(a.res, base + c * VE);
+        xv[k].template load<MBRT_NT_RMS>(a.x, base + c * VE);
+        if (RES) rv[k].template load<MBRT_NT_RMS>(a.res, base + c * VE);
     }
     for (int d = threadIdx.x; d < a.dim; d += kThreads) gs[d] = load1(a.gamma, a.gdt, d) * a.scale;
     float v[NC][VE];
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
             if (k < full || lane + G * k <= lastc) {
                 Vec<XDT, VE> t;
                 t.from_f32(v[k]);
-                t.store(a.sum_out, base + (lane + G * k) * VE);
+                t.template store<MBRT_NT_RMS>(a.sum_out, base + (lane + G * k) * VE);
             }
         }
     }
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
             for (int i = 0; i < VE; ++i) v[k][i] = v[k][i] * inv * gs[c * VE + i];
             Vec<ODT, VE> o;
             o.from_f32(v[k]);
-            o.store(a.out, base + c * VE);
+            o.template store<MBRT_NT_RMS>(a.out, base + c * VE);
         }
     }
 }
@@ -145,11 +146,12 @@ void launch_fast(const RmsArgs& a, hipStream_t st) {
 // Group width / chunks per lane for `nchunk` chunks; false when the row is too long.
 template <int XDT, int ODT, bool RES>
 bool launch_chunks(const RmsArgs& a, hipStream_t st) {
+    constexpr int G = MBRT_RMS_G;
     const int n = a.nchunk;
-    if (n <= 32) launch_fast<XDT, ODT, RES, 16, 2>(a, st);
-    else if (n <= 64) launch_fast<XDT, ODT, RES, 16, 4>(a, st);
-    else if (n <= 96) launch_fast<XDT, ODT, RES, 16, 6>(a, st);
-    else if (n <= 128) launch_fast<XDT, ODT, RES, 16, 8>(a, st);
+    if (n <= 2 * G) launch_fast<XDT, ODT, RES, G, 2>(a, st);
+    else if (n <= 4 * G) launch_fast<XDT, ODT, RES, G, 4>(a, st);
+    else if (n <= 6 * G) launch_fast<XDT, ODT, RES, G, 6>(a, st);
+    else if (n <= 128) launch_fast<XDT, ODT, RES, G, 128 / G>(a, st);
     else if (n <= 512) launch_fast<XDT, ODT, RES, 64, 8>(a, st);
     else if (n <= 1024) launch_fast<XDT, ODT, RES, 64, 16>(a, st);
     else return false;

@@ -57,8 +57,8 @@ __global__ __launch_bounds__(kThreads) void rotary_vec_kernel(RotArgs a) {
     const int64_t e = (int64_t)g * VE;
     Vec<DT, VE> q, k;
     Vec<TDT, VE / 2> cv, sv;
-    q.load(a.q, e);
-    if (HAS_K) k.load(a.k, e);
+    q.template load<MBRT_NT_ROT>(a.q, e);
+    if (HAS_K) k.template load<MBRT_NT_ROT>(a.k, e);
     cv.load(a.cosp, t);
     sv.load(a.sinp, t);
     float cs[VE / 2], sn[VE / 2], x[VE];
@@ -67,12 +67,12 @@ __global__ __launch_bounds__(kThreads) void rotary_vec_kernel(RotArgs a) {
     q.to_f32(x);
     rotate<VE>(x, cs, sn);
     q.from_f32(x);
-    q.store(a.q, e);
+    q.template store<MBRT_NT_ROT>(a.q, e);
     if (HAS_K) {
         k.to_f32(x);
         rotate<VE>(x, cs, sn);
         k.from_f32(x);
-        k.store(a.k, e);
+        k.template store<MBRT_NT_ROT>(a.k, e);
     }
 }
 
@@ -128,9 +128,9 @@ __global__ __launch_bounds__(kThreads) void split_qkv_vec_kernel(SplitArgs a, ui
     const int64_t t = nn * (a.D / 2) + (int64_t)c * (VE / 2);
     Vec<IDT, VE> vq, vk, vv;
     Vec<TDT, VE / 2> cv, sv;
-    vq.load(a.qkv, src);
-    vk.load(a.qkv, src + a.H * a.D);
-    vv.load(a.qkv, src + 2 * a.H * a.D);
+    vq.template load<MBRT_NT_ROT>(a.qkv, src);
+    vk.template load<MBRT_NT_ROT>(a.qkv, src + a.H * a.D);
+    vv.template load<MBRT_NT_ROT>(a.qkv, src + 2 * a.H * a.D);
     cv.load(a.cosp, t);
     sv.load(a.sinp, t);
     float xq[VE], xk[VE], xv[VE], cs[VE / 2], sn[VE / 2];
@@ -147,11 +147,11 @@ __global__ __launch_bounds__(kThreads) void split_qkv_vec_kernel(SplitArgs a, ui
     }
     Vec<ODT, VE> o;
     o.from_f32(xq);
-    o.store(a.q, e);
+    o.template store<MBRT_NT_ROT>(a.q, e);
     o.from_f32(xk);
-    o.store(a.k, e);
+    o.template store<MBRT_NT_ROT>(a.k, e);
     o.from_f32(xv);
-    o.store(a.v, e);
+    o.template store<MBRT_NT_ROT>(a.v, e);
 }
 
 __global__ __launch_bounds__(kThreads) void split_qkv_scalar_kernel(SplitArgs a) {

@@ -9,6 +9,9 @@
 // exp2 of the pre-scaled input (z * log2 e), one v_exp_f32 per element.
 //   801 cols : G = 64, 13 elements per lane, 4 rows per 256-thread block
 //   60 cols  : G = 16, 4 elements per lane, 16 rows per block
+// Short rows (<= 128 elements) are staged: a block owns 256 / G consecutive rows, one
+// contiguous span of the tensor, which it reads and writes with 16-byte vector accesses
+// through LDS, so a 60-element bf16 row (120 bytes) costs no 2-byte accesses.
 // Rows longer than 64 x 32 elements use a three-pass loop kernel.
 #include "abi_common.hpp"
 
@@ -42,7 +45,7 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
     const int last = a.cols - 1;
     float z[NM];
 #pragma unroll
-    for (int k = 0; k < NM; ++k) z[k] = ld1<IDT>(a.in, base + min(lane + G * k, last));
+    for (int k = 0; k < NM; ++k) z[k] = ld1<IDT, MBRT_NT_SMR>(a.in, base + min(lane + G * k, last));
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < NM; ++k) {
@@ -64,10 +67,86 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
         if (!valid) return;
 #pragma unroll
         for (int k = 0; k < NM; ++k) {
-            if (k < full || lane + G * k <= last) st1<ODT>(a.out, base + lane + G * k, z[k] * inv);
+            if (k < full || lane + G * k <= last) st1<ODT, MBRT_NT_SMR>(a.out, base + lane + G * k, z[k] * inv);
         }
     };
     with_dt(a.odt, store_all);
+}
+
+// Staged short rows.  Block b owns rows [b*RB, b*RB + RB), RB = 256 / G, i.e. the span of
+// RB*cols elements starting at element b*RB*cols.  The launcher only picks this kernel when
+// that span is a whole number of 16-byte vectors for the input and the output dtype, both
+// pointers are 16-byte aligned and rows*cols fills whole vectors, so every vector lies in
+// one block's span.  Phase 1 loads the span (clamped vector indices, predicated LDS
+// writes), phase 2 is the same register-resident group softmax as above but fed from LDS,
+// writing the probabilities back over their inputs, phase 3 stores the span.  In-place
+// calls are safe: the whole span is in LDS before its first store.
+template <int IDT, int ODT, int G, int NM>
+__global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
+    constexpr int RB = kThreads / G;
+    constexpr int VI = 16 / DtSize<IDT>::value, VO = 16 / DtSize<ODT>::value;
+    constexpr int CAP = RB * G * NM;  // floats of LDS (RB rows of at most G*NM elements)
+    constexpr int KI = (CAP / VI + kThreads - 1) / kThreads, KO = (CAP / VO + kThreads - 1) / kThreads;
+    __shared__ float buf[CAP];
+    const int tid = threadIdx.x;
+    const int64_t row0 = (int64_t)blockIdx.x * RB;
+    const int nrows = (int)min((int64_t)RB, a.rows - row0);
+    const int nel = nrows * a.cols;
+    const int64_t ebase = row0 * a.cols;
+    const int nvi = nel / VI;
+    Vec<IDT, VI> iv[KI];
+#pragma unroll
+    for (int k = 0; k < KI; ++k) iv[k].template load<MBRT_NT_SMS>(a.in, ebase + (int64_t)min(tid + kThreads * k, nvi - 1) * VI);
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+        const int v = tid + kThreads * k;
+        if (v < nvi) {
+            float f[VI];
+            iv[k].to_f32(f);
+#pragma unroll
+            for (int i = 0; i < VI; ++i) buf[v * VI + i] = f[i];
+        }
+    }
+    __syncthreads();
+    const int r = tid / G, lane = tid % G;
+    const int last = a.cols - 1;
+    const int rbase = min(r, nrows - 1) * a.cols;
+    float z[NM];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NM; ++k) {
+        const float x = buf[rbase + min(lane + G * k, last)];
+        z[k] = lane + G * k <= last ? x * a.scale_log2e : -INFINITY;
+        m = fmaxf(m, z[k]);
+    }
+    m = group_max<G>(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NM; ++k) {
+        z[k] = __builtin_amdgcn_exp2f(z[k] - m);
+        s += z[k];
+    }
+    s = group_sum<G>(s);
+    const float inv = 1.0f / s;
+    if (r < nrows) {
+#pragma unroll
+        for (int k = 0; k < NM; ++k)
+            if (lane + G * k <= last) buf[rbase + lane + G * k] = z[k] * inv;
+    }
+    __syncthreads();
+    const int nvo = nel / VO;
+#pragma unroll
+    for (int k = 0; k < KO; ++k) {
+        const int v = tid + kThreads * k;
+        if (v < nvo) {
+            float f[VO];
+#pragma unroll
+            for (int i = 0; i < VO; ++i) f[i] = buf[v * VO + i];
+            Vec<ODT, VO> o;
+            o.from_f32(f);
+            o.template store<MBRT_NT_SMS>(a.out, ebase + (int64_t)v * VO);
+        }
+    }
 }
 
 // Long rows: one wave per row, three passes (max, sum, write) over global memory.
@@ -87,6 +166,31 @@ __global__ __launch_bounds__(kThreads) void softmax_loop_kernel(SmArgs a, int id
     for (int64_t c = lane; c < a.cols; c += 64)
         store1(a.out, a.odt, start + c,
                __builtin_amdgcn_exp2f(load1(a.in, idt, start + c) * a.scale_log2e - m) * inv);
+}
+
+template <int IDT, int G, int NM>
+void launch_staged(const SmArgs& a, hipStream_t st) {
+    with_dt(a.odt, [&](auto ot) {
+        hipLaunchKernelGGL((softmax_staged_kernel<IDT, decltype(ot)::value, G, NM>),
+                           dim3((unsigned)ceil_div(a.rows, kThreads / G)), dim3(kThreads), 0, st, a);
+    });
+}
+
+// Staged path for rows of at most 128 elements, when every block span is made of whole
+// 16-byte vectors of both dtypes (see softmax_staged_kernel).
+template <int IDT>
+bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) {
+    const int c = a.cols;
+    if (c > 128 || !aligned(a.in, 16) || !aligned(a.out, 16)) return false;
+    const int rb = c <= 16 ? 64 : c <= 64 ? 32 : 16;
+    for (int es : {in_esize, out_esize}) {
+        if (((int64_t)rb * c * es) % 16 != 0 || (a.rows * c * es) % 16 != 0) return false;
+    }
+    if (c <= 16) launch_staged<IDT, 4, 4>(a, st);
+    else if (c <= 32) launch_staged<IDT, 8, 4>(a, st);
+    else if (c <= 64) launch_staged<IDT, 8, 8>(a, st);
+    else launch_staged<IDT, 16, 8>(a, st);
+    return true;
 }
 
 template <int IDT, int G, int NM>
@@ -138,10 +242,11 @@ int mbrt_softmax_rows(const void* in, int in_dtype, void* out, int out_dtype, in
     a.cols = (int)cols;
     a.scale_log2e = scale * kLog2e;
     hipStream_t st = as_stream(stream);
+    const int ies = dt_size(in_dtype), oes = dt_size(out_dtype);
     bool done;
-    if (in_dtype == F32) done = launch_fast<F32>(a, st);
-    else if (in_dtype == BF16) done = launch_fast<BF16>(a, st);
-    else done = launch_fast<F16>(a, st);
+    if (in_dtype == F32) done = launch_short<F32>(a, ies, oes, st) || launch_fast<F32>(a, st);
+    else if (in_dtype == BF16) done = launch_short<BF16>(a, ies, oes, st) || launch_fast<BF16>(a, st);
+    else done = launch_short<F16>(a, ies, oes, st) || launch_fast<F16>(a, st);
     if (!done) {
         hipLaunchKernelGGL(softmax_loop_kernel, dim3((unsigned)ceil_div(rows, kThreads / 64)), dim3(kThreads), 0, st, a,
                            in_dtype);

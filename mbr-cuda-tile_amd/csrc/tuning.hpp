@@ -1,0 +1,57 @@
+// Per-kernel launch shapes and cache policies, chosen by measurement on MI355X at the
+// MelBandRoformer chunk shapes (T = 801 frames, 60 bands, D = 384, 48060 token rows).
+// Every value can be overridden at build time (build.py -D NAME=VALUE) to re-tune.
+//
+// MBRT_NT_* : non-temporal policy of a kernel's streaming operands, bit 0 = loads,
+//             bit 1 = stores.  Operands that are re-read (gamma, bias, gate logits, cos/sin
+//             tables) always use ordinary accesses.  Measured with each op's calls back to
+//             back (so an op pays for its own write-backs from the 256 MB MALL): uniform
+//             policies 0..3 per kernel, the best kept; differences under ~3 % are noise.
+#pragma once
+
+#ifndef MBRT_NT_RMS
+#define MBRT_NT_RMS 3    // residual add + RMSNorm: x, residual, sum, normed
+#endif
+#ifndef MBRT_NT_ACT
+#define MBRT_NT_ACT 2    // bias + activation (GELU)
+#endif
+#ifndef MBRT_NT_GLU
+#define MBRT_NT_GLU 3
+#endif
+#ifndef MBRT_NT_GATE
+#define MBRT_NT_GATE 3   // sigmoid gate x head merge: attention values, merged output
+#endif
+#ifndef MBRT_NT_SMR
+#define MBRT_NT_SMR 0    // register-resident softmax rows (time attention, 801 columns)
+#endif
+#ifndef MBRT_NT_SMS
+#define MBRT_NT_SMS 3    // LDS-staged short softmax rows (freq attention, 60 columns)
+#endif
+#ifndef MBRT_NT_ROT
+#define MBRT_NT_ROT 3    // rotary q/k
+#endif
+#ifndef MBRT_NT_ROW
+#define MBRT_NT_ROW 3    // row copy (permutes that keep the innermost dim)
+#endif
+#ifndef MBRT_NT_TR
+#define MBRT_NT_TR 0     // LDS tile transpose
+#endif
+#ifndef MBRT_NT_EW
+#define MBRT_NT_EW 0     // convert / unary / scalar / binary vector kernels
+#endif
+#ifndef MBRT_NT_BAND
+#define MBRT_NT_BAND 2   // band gather / mask merge: stft, masks, outputs
+#endif
+
+#ifndef MBRT_ACT_U
+#define MBRT_ACT_U 1     // 16-byte groups per thread in the activation kernels
+#endif
+#ifndef MBRT_EW_U
+#define MBRT_EW_U 4      // 16-byte groups per thread in the elementwise kernels
+#endif
+#ifndef MBRT_ROW_U
+#define MBRT_ROW_U 2     // row-copy vectors per thread
+#endif
+#ifndef MBRT_RMS_G
+#define MBRT_RMS_G 16    // lanes per row for rows of at most 128 16-byte chunks (16 or 32)
+#endif

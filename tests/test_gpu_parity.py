@@ -383,6 +383,25 @@ def test_softmax_shapes(orc, dev, cols, idt, odt):
     assert_close(to_host(y, odt), orc.softmax(x, idt, odt, 0.125), odt, "softmax")
 
 
+@pytest.mark.parametrize("rows,cols", [(1000, 16), (1000, 17), (1000, 32), (1000, 60), (1000, 100), (1000, 128),
+                                       (2008, 60), (8, 60)])
+@pytest.mark.parametrize("idt,odt", [(F32, F32), (BF16, BF16), (F32, BF16), (BF16, F32), (F16, F16)])
+def test_softmax_short_rows(orc, dev, rows, cols, idt, odt):
+    """Row counts whose spans are whole 16-byte vectors (the LDS-staged short-row path),
+    with a partial last block, then the same call in place."""
+    say(f"softmax short rows={rows} cols={cols} {idt}->{odt}")
+    x = inp(orc, (rows, cols), 37, cols, idt, std=3.0)
+    xd = to_dev(x, idt)
+    y = empty((rows, cols), odt)
+    mbrt.softmax(xd, y, 0.5)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), orc.softmax(x, idt, odt, 0.5), odt, "softmax short")
+    if idt == odt:
+        mbrt.softmax(xd, xd, 0.5)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(xd, odt), to_host(y, odt), "softmax short in place")
+
+
 # ---- rotary --------------------------------------------------------------------------------
 
 def test_rotary_bl4a_full(orc, dev):
