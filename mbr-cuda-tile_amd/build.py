@@ -60,6 +60,7 @@ KERNEL_SOURCES = [
 
 TENSOR_SOURCES = [
     "hip_context.cpp",
+    "memory_pool.cpp",
     "tensor.cpp",
     "tensor_tile.cpp",
     "mbr_tile.cpp",
@@ -80,9 +81,10 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out)
 
 
-def _compile(src: Path, obj: Path, defines: list[str], verbose: bool) -> Path:
+def _compile(src: Path, obj: Path, defines: list[str], verbose: bool, extra: list[str] | None = None) -> Path:
     lang = ["-x", "hip"] if src.suffix in (".hip", ".cpp") else []
-    _run([HIPCC, *COMMON, *[f"-D{d}" for d in defines], *lang, "-c", str(src), "-o", str(obj)], verbose)
+    _run([HIPCC, *COMMON, *(extra or []), *[f"-D{d}" for d in defines], *lang, "-c", str(src), "-o", str(obj)],
+         verbose)
     return obj
 
 
@@ -95,7 +97,10 @@ def _objects(srcdir: Path, names: list[str], tag: str, build_dir: Path, defines:
         for n in names:
             src = srcdir / n
             obj = build_dir / f"{tag}_{Path(n).stem}.o"
-            futs.append(ex.submit(_compile, src, obj, defines, verbose))
+            # the C-ABI library exports only its MBRT_API symbols; the C++ tensor layer
+            # exports its whole API
+            extra = ["-fvisibility=default"] if tag == "t" else None
+            futs.append(ex.submit(_compile, src, obj, defines, verbose, extra))
         for f in futs:
             objs.append(f.result())
     return objs
@@ -127,14 +132,30 @@ def build(jobs: int | None = None, verbose: bool = False, defines: list[str] | N
     return out
 
 
+def build_selftest(verbose: bool = False, out_dir: Path | str | None = None) -> Path:
+    """Link tests/cpp/tensor_selftest.cpp against the libraries (test infrastructure: the
+    C++ layer's self-test, run by tests/test_cpp_layer.py on a GPU)."""
+    lib_dir = Path(out_dir) if out_dir else LIB
+    exe = lib_dir / "tensor_selftest"
+    src = REPO / "tests" / "cpp" / "tensor_selftest.cpp"
+    tmp = exe.with_suffix(".tmp")
+    _run([HIPCC, *COMMON, "-x", "hip", str(src), "-o", str(tmp), f"-L{lib_dir}", "-lmbrt_tensor", "-lmbrt",
+          "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp, exe)
+    return exe
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
     ap.add_argument("-v", action="store_true")
     ap.add_argument("-D", dest="defines", action="append", default=[], metavar="NAME=VALUE")
     ap.add_argument("--out", default=None, help="output directory (default: the package's lib/)")
+    ap.add_argument("--selftest", action="store_true", help="also link the C++ layer's self-test binary")
     a = ap.parse_args(argv)
     paths = build(a.j, a.v, a.defines, a.out)
+    if a.selftest and "libmbrt_tensor" in paths:
+        paths["tensor_selftest"] = build_selftest(a.v, a.out)
     for k, p in paths.items():
         print(f"{k}: {p}")
     return 0

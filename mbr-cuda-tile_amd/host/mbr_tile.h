@@ -1,0 +1,74 @@
+// cudasep::mbr_tile — the memory-bound MelBandRoformer ops of the reference's model
+// library (src/mbr_cuda_tile.h), same names, arguments and dtype policies, on libmbrt's
+// gfx950 kernels.  The GEMM and fused-attention entry points of that header are outside
+// this library; the epilogues they end in (bias + GELU / sigmoid, row softmax) are
+// exported as their own functions below.
+#pragma once
+
+#include <vector>
+
+#include "tensor.h"
+
+namespace cudasep::mbr_tile {
+
+// ---- precision policies (env switches and g_quantize_bf16, src/mbr_cuda_tile.cu:103-354)
+bool residual_bf16_enabled();
+bool bias_bf16_enabled();
+bool norm_gamma_bf16_enabled();
+bool bands_per_freq_bf16_enabled();
+bool rotary_freqs_bf16_enabled();
+bool residual_rms_norm_fused_path_enabled();
+
+// ---- normalisation
+// y = x * scale * gamma / sqrt(sum x^2 + 1e-12) over the last dim (src/mbr_cuda_tile.cu:6297-6373).
+// Output BF16 under the RMS-norm bf16 policy, else F32 (F16 for F16 input).
+Tensor rms_norm(const Tensor& x, const Tensor& gamma, float scale);
+
+// residual_out = residual + update (in residual's dtype), normed = rms_norm(residual_out)
+// in one pass (src/mbr_cuda_tile.cu:6375-6417).  Unlike the reference, which fuses only
+// bf16 rows of 256, every dim and dtype is fused; false is returned only when the fused
+// path is disabled (CUDASEP_DISABLE_RESIDUAL_RMS_NORM_FUSED) or the operands do not
+// match, and the caller then adds and normalises separately, as in the reference.
+bool try_residual_add_rms_norm(const Tensor& residual, const Tensor& update, const Tensor& gamma, float scale,
+                               Tensor& residual_out, Tensor& normed);
+
+// ---- attention plumbing
+// qkv [B, N, 3*heads*dim_head] -> q, k, v [B, heads, N', dim_head] with rotary on q and k
+// (src/mbr_cuda_tile.cu:6058-6213).  N' = 64 for the bf16 N = 60, D = 64 frequency
+// attention (zero rows 60..63), else N.
+void split_qkv_heads_rotary(const Tensor& qkv, int heads, int dim_head, const Tensor& cos_freqs,
+                            const Tensor& sin_freqs, Tensor& q, Tensor& k, Tensor& v);
+
+// In-place rotary on contiguous q, k [B, N, heads, dim_head] with cos/sin [N, dim_head/2]
+// (src/mbr_cuda_tile.cu:7454-7584), for any B, N, heads, even dim_head.
+void apply_rotary_time_split_contig_inplace(Tensor& q, Tensor& k, const Tensor& cos_freqs, const Tensor& sin_freqs);
+void apply_rotary_time_split_contig_k_only_inplace(Tensor& k, const Tensor& cos_freqs, const Tensor& sin_freqs);
+
+// merged[b, n, h*D + d] = attn[b, h, n, d] * gates[b, n, h] (src/mbr_cuda_tile.cu:6243-6295).
+Tensor apply_gates_and_merge_heads(const Tensor& attn, const Tensor& gates, int heads, int dim_head);
+// Same with the gate logits: sigmoid fused into the merge (linear_sigmoid's epilogue and
+// the merge in one pass).
+Tensor apply_gate_logits_and_merge_heads(const Tensor& attn, const Tensor& gate_logits, int heads, int dim_head);
+
+// Row softmax of attention scores over the last dim, p = softmax(scale * x), f32
+// accumulation (the scale_softmax kernels, src/mbr_cuda_tile.cu:5092-5285).
+Tensor softmax_last_dim(const Tensor& x, float scale, DType out_dtype);
+void softmax_last_dim_(Tensor& x, float scale);
+
+// ---- activations
+// act(x + bias) over the last dim, the linear-layer epilogues (src/mbr_cuda_tile.cu:5474-5584).
+enum class Activation { None = 0, GeluRef = 1, GeluStd = 2, Sigmoid = 3, Tanh = 4 };
+Tensor add_bias_activation(const Tensor& x, const Tensor* bias, Activation act, DType out_dtype);
+Tensor tanh_act(const Tensor& x);
+Tensor glu_last_dim(const Tensor& x);
+
+// ---- band split / merge
+Tensor gather_freqs_fold_complex(const Tensor& stft_repr, const Tensor& freq_indices);
+Tensor apply_mask_and_scatter(const Tensor& stft_repr, const std::vector<Tensor>& stem_masks,
+                              const Tensor& freq_indices, const Tensor& freq_band_offsets,
+                              const Tensor& freq_band_indices, const Tensor& bands_per_freq, int64_t batch,
+                              int64_t num_stems, int64_t total_freq, int64_t total_band_freqs, int64_t frames,
+                              int64_t audio_channels, int64_t max_bands_per_freq = 0);
+void zero_dc(Tensor& complex_spec);
+
+}  // namespace cudasep::mbr_tile

@@ -1,0 +1,186 @@
+"""Tests of the C++ tensor layer (cudasep::Tensor, tensor_tile::, mbr_tile::) that callers
+of the reference's C++ API link against (mbr-cuda-tile_amd/lib/libmbrt_tensor.so).
+
+CPU: the library exports the reference's C++ API.  GPU: tensor_selftest checks Tensor
+semantics against host expectations, then runs the mbr_tile ops on inputs written here
+and their outputs are compared with the oracle."""
+from __future__ import annotations
+
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from parity import BF16, F32, I64, assert_bitexact, assert_close, merge_den
+
+REPO = Path(__file__).resolve().parent.parent
+LIB = REPO / "mbr-cuda-tile_amd" / "lib"
+SELFTEST = LIB / "tensor_selftest"
+TENSOR_LIB = LIB / "libmbrt_tensor.so"
+
+# Reference C++ entry points (src/tensor.h, src/tensor_cuda_tile.h, src/mbr_cuda_tile.h)
+# the layer must define.
+API = [
+    "cudasep::Tensor::empty(", "cudasep::Tensor::zeros(", "cudasep::Tensor::ones(", "cudasep::Tensor::full(",
+    "cudasep::Tensor::arange(", "cudasep::Tensor::from_cpu_f32(", "cudasep::Tensor::from_cpu_f16(",
+    "cudasep::Tensor::from_cpu_i64(", "cudasep::Tensor::reshape(", "cudasep::Tensor::permute(",
+    "cudasep::Tensor::transpose(", "cudasep::Tensor::contiguous() const", "cudasep::Tensor::unsqueeze(",
+    "cudasep::Tensor::squeeze(", "cudasep::Tensor::expand(", "cudasep::Tensor::slice(",
+    "cudasep::Tensor::index_select(", "cudasep::Tensor::cat(", "cudasep::Tensor::stack(", "cudasep::Tensor::split(",
+    "cudasep::Tensor::unbind(", "cudasep::Tensor::pad(", "cudasep::Tensor::pad_reflect(", "cudasep::Tensor::to_dtype(",
+    "cudasep::Tensor::operator+(", "cudasep::Tensor::operator-(", "cudasep::Tensor::operator*(",
+    "cudasep::Tensor::operator/(", "cudasep::Tensor::add_(", "cudasep::Tensor::mul_(", "cudasep::Tensor::add_scalar_(",
+    "cudasep::Tensor::mul_scalar_(", "cudasep::Tensor::clamp_(", "cudasep::Tensor::fill_(", "cudasep::Tensor::sum(",
+    "cudasep::Tensor::mean(", "cudasep::Tensor::max(", "cudasep::Tensor::operator>(", "cudasep::Tensor::clone() const",
+    "cudasep::Tensor::copy_from(", "cudasep::Tensor::to_cpu_f32() const", "cudasep::Tensor::copy_from_cpu(",
+    "cudasep::Tensor::copy_to_cpu(", "cudasep::Tensor::is_contiguous() const", "cudasep::Tensor::print(",
+    "cudasep::tensor_tile::fill(", "cudasep::tensor_tile::arange(", "cudasep::tensor_tile::convert_dtype(",
+    "cudasep::tensor_tile::add_scalar(", "cudasep::tensor_tile::mul_scalar(", "cudasep::tensor_tile::clamp(",
+    "cudasep::tensor_tile::negate(", "cudasep::tensor_tile::greater_than(", "cudasep::tensor_tile::binary_same_shape(",
+    "cudasep::tensor_tile::binary_inplace_same_shape(", "cudasep::tensor_tile::binary_glue(",
+    "cudasep::tensor_tile::binary_inplace_glue(", "cudasep::tensor_tile::index_select_glue(",
+    "cudasep::tensor_tile::strided_copy_glue(", "cudasep::tensor_tile::pad_const_glue(",
+    "cudasep::tensor_tile::pad_reflect_glue(", "cudasep::tensor_tile::cat_glue(",
+    "cudasep::tensor_tile::sum_reduce_last_dim(", "cudasep::tensor_tile::max_reduce_last_dim(",
+    "cudasep::tensor_tile::sum_reduce_general_glue(", "cudasep::tensor_tile::max_reduce_general_glue(",
+    "cudasep::mbr_tile::rms_norm(", "cudasep::mbr_tile::try_residual_add_rms_norm(",
+    "cudasep::mbr_tile::residual_rms_norm_fused_path_enabled(", "cudasep::mbr_tile::apply_gates_and_merge_heads(",
+    "cudasep::mbr_tile::split_qkv_heads_rotary(", "cudasep::mbr_tile::apply_rotary_time_split_contig_inplace(",
+    "cudasep::mbr_tile::apply_rotary_time_split_contig_k_only_inplace(",
+    "cudasep::mbr_tile::gather_freqs_fold_complex(", "cudasep::mbr_tile::apply_mask_and_scatter(",
+    "cudasep::mbr_tile::glu_last_dim(", "cudasep::mbr_tile::tanh_act(", "cudasep::mbr_tile::zero_dc(",
+    "cudasep::mbr_tile::residual_bf16_enabled(", "cudasep::mbr_tile::bias_bf16_enabled(",
+    "cudasep::mbr_tile::norm_gamma_bf16_enabled(", "cudasep::mbr_tile::bands_per_freq_bf16_enabled(",
+    "cudasep::mbr_tile::rotary_freqs_bf16_enabled(", "cudasep::HipMemoryPool::allocate(",
+    "cudasep::HipMemoryPool::deallocate(", "cudasep::HipMemoryPool::trim_cached_memory(",
+]
+
+
+def test_tensor_layer_exports_reference_api():
+    assert TENSOR_LIB.exists(), "run python mbr-cuda-tile_amd/build.py"
+    out = subprocess.run(["nm", "-DC", "--defined-only", str(TENSOR_LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    missing = [name for name in API if name not in out]
+    assert not missing, f"missing C++ entry points: {missing}"
+
+
+def test_tensor_layer_links_only_the_c_abi():
+    """The C++ layer reaches the GPU kernels through libmbrt's C-ABI only."""
+    out = subprocess.run(["nm", "-DC", "--undefined-only", str(TENSOR_LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    used = sorted({ln.split()[-1] for ln in out.splitlines() if "mbrt_" in ln})
+    assert used and all(u.startswith("mbrt_") for u in used), used
+    assert SELFTEST.exists()
+
+
+def _selftest(*args, timeout=120):
+    return subprocess.run([str(SELFTEST), *args], capture_output=True, text=True, timeout=timeout)
+
+
+@pytest.mark.gpu
+def test_tensor_unit_semantics(dev):
+    r = _selftest("unit")
+    print(r.stdout)
+    fails = [ln for ln in r.stdout.splitlines() if ln.startswith("FAIL")]
+    assert r.returncode == 0 and not fails, (r.returncode, fails, r.stderr[-2000:])
+
+
+def _write(dirp: Path, manifest: list, name: str, arr: np.ndarray, dt: int):
+    arr = np.ascontiguousarray(arr)
+    (dirp / f"{name}.bin").write_bytes(arr.tobytes())
+    manifest.append(f"{name} {dt} {arr.ndim} {' '.join(str(s) for s in arr.shape)}")
+
+
+def _read(dirp: Path, name: str):
+    meta = (dirp / f"{name}.meta").read_text().split()
+    dt, shape = int(meta[0]), tuple(int(s) for s in meta[1:])
+    np_dt = {F32: np.float32, BF16: np.uint16}[dt]
+    return dt, np.fromfile(dirp / f"{name}.out", dtype=np_dt).reshape(shape)
+
+
+@pytest.mark.gpu
+def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
+    rng_seed = 0x4D425200C0
+    R, D = 300, 384
+    x = orc.randn((R, D), seed=rng_seed, stream=1)
+    res = orc.randn((R, D), seed=rng_seed, stream=2)
+    gamma = orc.randn((D,), seed=rng_seed, stream=3, mean=1.0, std=0.02)
+    scores = orc.randn((97, 60), seed=rng_seed, stream=4, std=3.0)
+    h = orc.randn((64, 1536), seed=rng_seed, stream=5, std=1.5)
+    bias = orc.randn((1536,), seed=rng_seed, stream=6, std=0.1)
+    g = orc.from_f32(orc.randn((50, 3072), seed=rng_seed, stream=7, std=1.5), BF16)
+    B, H, N, Dh = 2, 8, 60, 64
+    attn = orc.from_f32(orc.randn((B, H, N, Dh), seed=rng_seed, stream=8), BF16)
+    logits = orc.randn((B, N, H), seed=rng_seed, stream=9, std=2.0)
+    gates = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    gates = gates.astype(np.float32)
+    q = orc.from_f32(orc.randn((B, N, H, Dh), seed=rng_seed, stream=10), BF16)
+    k = orc.from_f32(orc.randn((B, N, H, Dh), seed=rng_seed, stream=11), BF16)
+    cos, sin = orc.rotary_tables(N, Dh)
+    qkv = orc.from_f32(orc.randn((B, N, 3 * H * Dh), seed=rng_seed, stream=12), BF16)
+    mb = orc.mel_bands(44100.0, 2048, 60, 2)
+    Bb, F, T = 2, 2050, 37
+    J = mb["freq_indices"].size
+    stft = orc.randn((Bb, F, T, 2), seed=rng_seed, stream=13)
+    m0 = orc.randn((Bb, T, J * 2), seed=rng_seed, stream=14, std=0.5)
+    m1 = orc.randn((Bb, T, J * 2), seed=rng_seed, stream=15, std=0.5)
+    cnt = mb["bands_per_freq"].astype(np.float32)
+
+    man: list[str] = []
+    for name, arr, dt in [("x", x, F32), ("res", res, F32), ("gamma", gamma, F32), ("scores", scores, F32),
+                          ("h", h, F32), ("bias", bias, F32), ("g", g, BF16), ("attn", attn, BF16),
+                          ("logits", logits, F32), ("gates", gates, F32), ("q", q, BF16), ("k", k, BF16),
+                          ("cos", cos, F32), ("sin", sin, F32), ("qkv", qkv, BF16), ("stft", stft, F32),
+                          ("mask0", m0, F32), ("mask1", m1, F32), ("counts", cnt, F32),
+                          ("freq_indices", mb["freq_indices"].astype(np.int64), I64),
+                          ("csr_off", mb["csr_offsets"].astype(np.int64), I64),
+                          ("csr_ind", mb["csr_indices"].astype(np.int64), I64)]:
+        _write(tmp_path, man, name, arr, dt)
+    (tmp_path / "manifest.txt").write_text("\n".join(man) + "\n")
+    r = _selftest("ops", str(tmp_path))
+    print(r.stdout)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+
+    scale = float(np.float32(np.sqrt(np.float32(384.0))))
+    dt, y = _read(tmp_path, "rms_norm")
+    assert dt == F32
+    assert_close(y, orc.rms_norm(x, F32, gamma, F32, F32, scale, 1e-12), F32, "rms_norm")
+    ref_n, ref_s = orc.rms_norm(x, F32, gamma, F32, F32, scale, 1e-12, res=res, sdt=F32, want_sum=True)
+    assert_close(_read(tmp_path, "resid_sum")[1], ref_s, F32, "residual sum")
+    assert_close(_read(tmp_path, "resid_normed")[1], ref_n, F32, "residual normed")
+    ref_sm = orc.softmax(scores, F32, F32, 0.125)
+    assert_close(_read(tmp_path, "softmax")[1], ref_sm, F32, "softmax")
+    assert_bitexact(_read(tmp_path, "softmax_inplace")[1], _read(tmp_path, "softmax")[1], "softmax in place")
+    dt, y = _read(tmp_path, "gelu_ref")
+    assert dt == BF16
+    assert_close(y, orc.bias_act(h, F32, bias, F32, BF16, 1), BF16, "gelu ref")
+    dt, y = _read(tmp_path, "gather")
+    assert dt == F32
+    assert_bitexact(y, orc.band_gather(stft, mb["freq_indices"], F32, Bb, F, T), "gather")
+    ref_m = orc.band_mask_merge(stft, [m0.reshape(Bb, T, J, 2), m1.reshape(Bb, T, J, 2)], F32, mb["csr_offsets"],
+                                mb["csr_indices"], cnt, F32, F32, Bb, F, T, 2)
+    assert_close(_read(tmp_path, "merge")[1], ref_m, F32, "merge",
+                 den=merge_den(orc, stft, [m0, m1], mb, Bb, F, T, 2))
+    ref_m1 = orc.band_mask_merge(stft, [m0.reshape(Bb, T, J, 2)], F32, mb["csr_offsets"], mb["csr_indices"], cnt,
+                                 F32, F32, Bb, F, T, 2)
+    assert_close(_read(tmp_path, "merge_rebuilt_csr")[1], ref_m1, F32, "merge (CSR rebuilt from freq_indices)",
+                 den=merge_den(orc, stft, [m0], mb, Bb, F, T, 2))
+    spec = stft.reshape(Bb * 2, F // 2, T, 2)
+    assert_bitexact(_read(tmp_path, "zero_dc")[1], orc.zero_dc(spec, F32), "zero_dc")
+    dt, y = _read(tmp_path, "glu_bf16")
+    assert dt == BF16
+    assert_close(y, orc.glu(g, BF16, BF16), BF16, "glu bf16")
+    assert_close(_read(tmp_path, "gates_merge")[1], orc.gate_merge(attn, BF16, gates, F32, BF16, B, H, N, Dh,
+                                                                   logit=False), BF16, "gate merge")
+    assert_close(_read(tmp_path, "gate_logits_merge")[1], orc.gate_merge(attn, BF16, logits, F32, BF16, B, H, N, Dh,
+                                                                         logit=True), BF16, "gate logits merge")
+    rq, rk = orc.rotary(q, k, BF16, cos, sin, F32, N, H, layout=1)
+    assert_close(_read(tmp_path, "rot_q")[1], rq, BF16, "rotary q")
+    assert_close(_read(tmp_path, "rot_k")[1], rk, BF16, "rotary k")
+    sq, sk, sv = orc.split_qkv(qkv, BF16, cos, sin, F32, BF16, B, N, H, Dh, 64)
+    for name, ref in (("split_q", sq), ("split_k", sk), ("split_v", sv)):
+        dt, y = _read(tmp_path, name)
+        assert dt == BF16 and y.shape == (B, H, 64, Dh), (name, y.shape)
+        assert_close(y, ref, BF16, name)
