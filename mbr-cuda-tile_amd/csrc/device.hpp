@@ -197,6 +197,29 @@ __device__ __forceinline__ void fdivmod(uint32_t n, const FastDiv& f, uint32_t& 
     r = n - q * f.d;
 }
 
+// MI355X deals the workgroups of a launch to its 8 XCDs round-robin (block p runs on XCD
+// p % 8), and each XCD has its own L2.  xcd_tile maps the linear block id p of an n-block
+// launch to a tile id so that every XCD walks one contiguous range of tile ids in order:
+// neighbouring tiles, which share cache lines at their edges, then meet in one L2 instead
+// of being fetched from HBM once per XCD.  The map is a bijection of [0, n).
+constexpr uint32_t kXcds = 8;
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t p, uint32_t n) {
+    const uint32_t x = p % kXcds, i = p / kXcds;
+    const uint32_t q = n / kXcds, r = n % kXcds;
+    return x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
+// Runs of G consecutive tiles per XCD, the launch as a whole still sweeping the tiles in
+// order: within each group of 8*G blocks, XCD x takes tiles x*G .. x*G+G-1.  Blocks past
+// the last whole group keep their own id.  A bijection of [0, n).
+template <uint32_t G>
+__device__ __forceinline__ uint32_t xcd_runs(uint32_t p, uint32_t n) {
+    constexpr uint32_t kGroup = kXcds * G;
+    if (G <= 1 || p >= n / kGroup * kGroup) return p;
+    const uint32_t base = p / kGroup * kGroup, q = p % kGroup;
+    return base + (q % kXcds) * G + q / kXcds;
+}
+
 // ---- wave64 reductions -----------------------------------------------------------
 // Groups of G consecutive lanes (G in {1,2,4,8,16,32,64}) reduce together and every lane
 // of a group receives the group's result.  Steps within a 16-lane row are DPP operand

@@ -50,6 +50,7 @@ struct GatherArgs {
     void* out;
     int odt;
     int64_t F, T, J;
+    uint32_t tiles_j, tiles_t, tiles;  // tile grid: band-bin tiles fastest, then frames, then batch
 };
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / 64); }
@@ -78,20 +79,33 @@ __device__ __forceinline__ f32x2 load_complex(const void* p, int64_t i) {
 template <int ODT, bool I64>
 __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
     __shared__ f32x2 tile[kTJ][kTT + 1];
-    const int64_t j0 = (int64_t)blockIdx.x * kTJ;
-    const int64_t t0 = (int64_t)blockIdx.y * kTT;
-    const int64_t b = blockIdx.z;
+    // one linear grid; neighbouring band-bin tiles (which read the same stft rows where
+    // bands overlap) run on one XCD
+    const uint32_t tid = xcd_runs<MBRT_BAND_XCD>(blockIdx.x, a.tiles);
+    const uint32_t tj = tid % a.tiles_j, rest = tid / a.tiles_j;
+    const int64_t j0 = (int64_t)tj * kTJ;
+    const int64_t t0 = (int64_t)(rest % a.tiles_t) * kTT;
+    const int64_t b = rest / a.tiles_t;
     const int lane = threadIdx.x % 64;
     const int w = wave_id();
-    const int f_lane = ld_idx<I64>(a.idx, min(j0 + lane, a.J - 1));
     const int64_t tq = min(t0 + lane, a.T - 1);
     const f32x2* stft = reinterpret_cast<const f32x2*>(a.stft) + b * a.F * a.T + tq;
     constexpr int kR = kTJ / (kThreads / 64);  // 16 rows per wave
     f32x2 v[kR];
+    if constexpr (MBRT_BAND_SLOAD) {
+        // the row indices of a wave are uniform: scalar loads through the constant cache
+        int64_t f[kR];
 #pragma unroll
-    for (int r = 0; r < kR; ++r) {
-        const int64_t f = __builtin_amdgcn_readlane(f_lane, w + 4 * r);
-        v[r] = gld<MBRT_NT_BAND>(stft + f * a.T);
+        for (int r = 0; r < kR; ++r) f[r] = ld_idx<I64>(a.idx, min(j0 + w + 4 * r, a.J - 1));
+#pragma unroll
+        for (int r = 0; r < kR; ++r) v[r] = gld<MBRT_NT_BAND>(stft + f[r] * a.T);
+    } else {
+        const int f_lane = ld_idx<I64>(a.idx, min(j0 + lane, a.J - 1));
+#pragma unroll
+        for (int r = 0; r < kR; ++r) {
+            const int64_t f = __builtin_amdgcn_readlane(f_lane, w + 4 * r);
+            v[r] = gld<MBRT_NT_BAND>(stft + f * a.T);
+        }
     }
 #pragma unroll
     for (int r = 0; r < kR; ++r) tile[w + 4 * r][lane] = v[r];
@@ -117,6 +131,7 @@ struct MergeArgs {
     int S;
     int F, T, J;
     FastDiv C;  // audio channels: freq = bin * C + ch
+    uint32_t tiles_f, tiles_t, tiles;  // tile grid: freq tiles fastest, then frames, then b*S+s
 };
 
 // Block (t-tile, f-tile, b*S+s).  Wave w owns freqs f0+w, f0+w+4, ... (8 of them) and lane
@@ -128,9 +143,13 @@ struct MergeArgs {
 template <int MDT, int ODT, bool I64>
 __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     __shared__ f32x2 ms[kME][kTT + 1];
-    const int t0 = blockIdx.x * kTT;
-    const int f0 = blockIdx.y * kTF;
-    const int bs = blockIdx.z;  // b * S + s
+    // one linear grid; neighbouring freq tiles (whose CSR runs split cache lines of the
+    // mask rows) run on one XCD
+    const uint32_t tile = xcd_runs<MBRT_BAND_XCD>(blockIdx.x, a.tiles);
+    const uint32_t tf = tile % a.tiles_f, rest = tile / a.tiles_f;
+    const int f0 = (int)tf * kTF;
+    const int t0 = (int)(rest % a.tiles_t) * kTT;
+    const int bs = (int)(rest / a.tiles_t);  // b * S + s
     const int b = a.S == 2 ? bs >> 1 : bs;
     const void* mask = a.mask[bs - b * a.S];
     const int lane = threadIdx.x % 64;
@@ -141,11 +160,25 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     const int t = t0 + lane;
     const int tq = min(t, a.T - 1);
 
-    const int off_lane = ld_idx<I64>(a.off, f0 + min(lane, nf));
+    // CSR offsets of the tile's freqs: uniform scalar loads, or lane l holds off[f0 + l]
+    int off_s[kPer + 1];
+    int off_lane = 0;
+    int e_begin, e_end;
+    if constexpr (MBRT_BAND_SLOAD) {
+        e_begin = ld_idx<I64>(a.off, f0);
+        e_end = ld_idx<I64>(a.off, f0 + nf);
+    } else {
+        off_lane = ld_idx<I64>(a.off, f0 + min(lane, nf));
+        e_begin = __builtin_amdgcn_readlane(off_lane, 0);
+        e_end = __builtin_amdgcn_readlane(off_lane, nf);
+    }
     float c = load1(a.cnt, a.cdt, f0 + min(lane, nf - 1));
     const float inv_lane = 1.0f / (c > 1.0e-8f ? c : 1.0e-8f);
-    const int e_begin = __builtin_amdgcn_readlane(off_lane, 0);
-    const int e_end = __builtin_amdgcn_readlane(off_lane, nf);
+    if constexpr (MBRT_BAND_SLOAD) {
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) off_s[r] = ld_idx<I64>(a.off, f0 + min(w + 4 * r, nf));
+        off_s[kPer] = 0;
+    }
 
     const f32x2* srow = reinterpret_cast<const f32x2*>(a.stft) + ((int64_t)b * a.F + f0) * a.T + tq;
     f32x2 sv[kPer], acc[kPer];
@@ -168,8 +201,14 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
             const int fl = w + 4 * r;  // local freq (wave-uniform); entries [off[f], off[f+1])
-            const int lo = max(__builtin_amdgcn_readlane(off_lane, fl), c0);
-            const int hi = fl < nf ? min(__builtin_amdgcn_readlane(off_lane, fl + 1), c1) : lo;
+            int lo, hi;
+            if constexpr (MBRT_BAND_SLOAD) {
+                lo = max(off_s[r], c0);
+                hi = fl < nf ? min(ld_idx<I64>(a.off, f0 + fl + 1), c1) : lo;
+            } else {
+                lo = max(__builtin_amdgcn_readlane(off_lane, fl), c0);
+                hi = fl < nf ? min(__builtin_amdgcn_readlane(off_lane, fl + 1), c1) : lo;
+            }
             for (int e = lo; e < hi; ++e) {
                 const f32x2 m = ms[e - c0][lane];
                 acc[r].x += sv[r].x * m.x - sv[r].y * m.y;
@@ -226,9 +265,13 @@ int mbrt_band_gather(const float* stft, const void* freq_indices, int index_dtyp
     MBRT_REQUIRE(stft && freq_indices && out, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
     MBRT_REQUIRE(aligned(stft, 8) && aligned(out, out_dtype == F32 ? 8 : 4), MBRT_E_ALIGN,
                  "%s: complex buffers must be aligned to one complex value", op);
-    MBRT_REQUIRE(B <= 65535, MBRT_E_SHAPE, "%s: batch %lld exceeds 65535", op, (long long)B);
-    GatherArgs a{stft, freq_indices, index_dtype == I64, out, out_dtype, total_freq, frames, n_band_freqs};
-    const dim3 grid((unsigned)ceil_div(n_band_freqs, kTJ), (unsigned)ceil_div(frames, kTT), (unsigned)B);
+    GatherArgs a{stft, freq_indices, index_dtype == I64, out, out_dtype, total_freq, frames, n_band_freqs, 0, 0, 0};
+    const int64_t tiles = ceil_div(n_band_freqs, kTJ) * ceil_div(frames, kTT) * B;
+    MBRT_REQUIRE(tiles < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many tiles", op);
+    a.tiles_j = (uint32_t)ceil_div(n_band_freqs, kTJ);
+    a.tiles_t = (uint32_t)ceil_div(frames, kTT);
+    a.tiles = (uint32_t)tiles;
+    const dim3 grid(a.tiles);
     with_dt(out_dtype, [&](auto ot) {
         constexpr int O = decltype(ot)::value;
         if (index_dtype == I64) hipLaunchKernelGGL((band_gather_kernel<O, true>), grid, dim3(kThreads), 0, as_stream(stream), a);
@@ -254,7 +297,6 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
     MBRT_REQUIRE(stft && masks && csr_offsets && counts && out && (n_band_freqs == 0 || csr_indices),
                  MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
     for (int s = 0; s < num_stems; ++s) MBRT_REQUIRE(masks[s] != nullptr, MBRT_E_INVALID_ARG, "%s: NULL mask", op);
-    MBRT_REQUIRE(B * num_stems <= 65535, MBRT_E_SHAPE, "%s: batch*stems exceeds 65535", op);
     MBRT_REQUIRE(total_freq < (1 << 30) && frames < (1 << 30) && n_band_freqs < (1 << 30) && B * frames < (1 << 30),
                  MBRT_E_SHAPE, "%s: dimension exceeds 2^30", op);
     MergeArgs a{};
@@ -271,7 +313,12 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
     a.T = (int)frames;
     a.J = (int)std::max<int64_t>(n_band_freqs, 1);
     a.C = make_fastdiv((uint32_t)channels);
-    const dim3 grid((unsigned)ceil_div(frames, kTT), (unsigned)ceil_div(total_freq, kTF), (unsigned)(B * num_stems));
+    const int64_t tiles = ceil_div(total_freq, kTF) * ceil_div(frames, kTT) * B * num_stems;
+    MBRT_REQUIRE(tiles < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many tiles", op);
+    a.tiles_f = (uint32_t)ceil_div(total_freq, kTF);
+    a.tiles_t = (uint32_t)ceil_div(frames, kTT);
+    a.tiles = (uint32_t)tiles;
+    const dim3 grid(a.tiles);
     with_dt(mask_dtype, [&](auto mt) {
         with_dt(out_dtype, [&](auto ot) {
             constexpr int M = decltype(mt)::value, O = decltype(ot)::value;

@@ -9,9 +9,10 @@
 // exp2 of the pre-scaled input (z * log2 e), one v_exp_f32 per element.
 //   801 cols : G = 64, 13 elements per lane, 4 rows per 256-thread block
 //   60 cols  : G = 16, 4 elements per lane, 16 rows per block
-// Short rows (<= 128 elements) are staged: a block owns 256 / G consecutive rows, one
-// contiguous span of the tensor, which it reads and writes with 16-byte vector accesses
-// through LDS, so a 60-element bf16 row (120 bytes) costs no 2-byte accesses.
+// Rows of at most 1024 elements are staged when the spans align: a block owns 256 / G
+// consecutive rows, one contiguous span of the tensor, which it reads and writes with
+// 16-byte vector accesses through LDS, so a 60-element bf16 row (120 bytes) or an
+// 801-element one (1602 bytes) costs no 2-byte accesses.
 // Rows longer than 64 x 32 elements use a three-pass loop kernel.
 #include "abi_common.hpp"
 
@@ -176,20 +177,37 @@ void launch_staged(const SmArgs& a, hipStream_t st) {
     });
 }
 
-// Staged path for rows of at most 128 elements, when every block span is made of whole
-// 16-byte vectors of both dtypes (see softmax_staged_kernel).
+// Staged path: rows of at most 1024 elements, when every block span is made of whole
+// 16-byte vectors of both dtypes (see softmax_staged_kernel).  Short rows use narrow
+// groups (many rows per block); rows of 129..1024 use 64 lanes per row (4 rows per block)
+// or, when 4 rows do not fill whole vectors (bf16 rows of odd length), 32 lanes (8 rows).
 template <int IDT>
 bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) {
     const int c = a.cols;
-    if (c > 128 || !aligned(a.in, 16) || !aligned(a.out, 16)) return false;
-    const int rb = c <= 16 ? 64 : c <= 64 ? 32 : 16;
-    for (int es : {in_esize, out_esize}) {
-        if (((int64_t)rb * c * es) % 16 != 0 || (a.rows * c * es) % 16 != 0) return false;
+    if (c > 1024 || !aligned(a.in, 16) || !aligned(a.out, 16)) return false;
+    auto fits = [&](int rb) {
+        for (int es : {in_esize, out_esize})
+            if (((int64_t)rb * c * es) % 16 != 0 || (a.rows * c * es) % 16 != 0) return false;
+        return true;
+    };
+    if (c <= 16 && fits(64)) launch_staged<IDT, 4, 4>(a, st);
+    else if (c <= 32 && fits(32)) launch_staged<IDT, 8, 4>(a, st);
+    else if (c <= 64 && fits(32)) launch_staged<IDT, 8, 8>(a, st);
+    else if (c <= 128 && fits(16)) launch_staged<IDT, 16, 8>(a, st);
+    else if (c <= 128 || !MBRT_SM_STAGE_LONG) return false;
+    else if (fits(4)) {
+        if (c <= 256) launch_staged<IDT, 64, 4>(a, st);
+        else if (c <= 512) launch_staged<IDT, 64, 8>(a, st);
+        else if (c <= 832) launch_staged<IDT, 64, 13>(a, st);
+        else launch_staged<IDT, 64, 16>(a, st);
+    } else if (fits(8)) {
+        if (c <= 256) launch_staged<IDT, 32, 8>(a, st);
+        else if (c <= 512) launch_staged<IDT, 32, 16>(a, st);
+        else if (c <= 832) launch_staged<IDT, 32, 26>(a, st);
+        else launch_staged<IDT, 32, 32>(a, st);
+    } else {
+        return false;
     }
-    if (c <= 16) launch_staged<IDT, 4, 4>(a, st);
-    else if (c <= 32) launch_staged<IDT, 8, 4>(a, st);
-    else if (c <= 64) launch_staged<IDT, 8, 8>(a, st);
-    else launch_staged<IDT, 16, 8>(a, st);
     return true;
 }
 

@@ -43,6 +43,15 @@
 #define MBRT_NT_BAND 2   // band gather / mask merge: stft, masks, outputs
 #endif
 
+#ifndef MBRT_BAND_XCD
+#define MBRT_BAND_XCD 8  // band kernels: runs of this many consecutive tiles per XCD (1: launch order)
+#endif
+#ifndef MBRT_BAND_SLOAD
+#define MBRT_BAND_SLOAD 0  // band gather: row indices by scalar loads (1) or lane load + readlane (0)
+#endif
+#ifndef MBRT_SM_STAGE_LONG
+#define MBRT_SM_STAGE_LONG 1  // softmax rows of 129..1024 elements through LDS when spans align
+#endif
 #ifndef MBRT_ACT_U
 #define MBRT_ACT_U 1     // 16-byte groups per thread in the activation kernels
 #endif
