@@ -38,6 +38,7 @@ sys.path.insert(0, str(REPO / "mbr-cuda-tile_amd"))
 
 METRIC = "achieved HBM GB/s (% of MI355X peak) per op; ms of tensor ops per chunk"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
 MALL_DEFEAT_BYTES = 1.1e9
 TRAFFIC_SUMMARY = REPO / "profiles" / "traffic_softmax_time_f32.md"
 
@@ -62,6 +63,8 @@ class Op:
         self.make = make         # () -> buffer set (dict)
         self.kernel = kernel     # kernel symbol substring (for the rocprof cross-check)
         self.sets = []
+        self.flops = 0.0
+        self.next = False
         self.run = None          # (buffer set) -> None
         self.times_ms = []
 
@@ -153,6 +156,18 @@ def build_ops(torch, mbrt, bands):
                          y=torch.empty((Bb * 2, F // 2, T, 2), device=dev)), "band_merge_kernel")
     op.run = lambda b: mbrt.band_mask_merge(b["s"], [b["m"]], off, ind, cnt, b["y"], 2)
     ops.append(op)
+    # Fused attention (MFMA), the first widening beyond the tensor-op path: q, k, v bf16
+    # [BH, N, 64] for the time (480 x 801) and frequency (6408 x 60) attention.  Reported in
+    # config.next_ops with TFLOP/s (4 BH N^2 64 flop); not part of `value`.
+    for tag, BH, N in (("time", 480, 801), ("freq", 6408, 60)):
+        op = Op(f"attention_{tag}_bf16", 4 * BH * N * 64 * 2,
+                (lambda BH=BH, N=N: dict(q=randn((BH, N, 64), bf16), k=randn((BH, N, 64), bf16),
+                                         v=randn((BH, N, 64), bf16), y=torch.empty((BH, N, 64), dtype=bf16, device=dev))),
+                "attention_kernel")
+        op.flops = 4.0 * BH * N * N * 64
+        op.next = True
+        op.run = lambda b: mbrt.attention(b["q"], b["k"], b["v"], b["y"], 0.125)
+        ops.append(op)
     return ops
 
 
@@ -316,8 +331,16 @@ def main():
         op.times_ms.append(e0.elapsed_time(e1))
 
     per_op = {}
+    next_ops = {}
     tot_bytes = 0
     tot_ms = 0.0
+    for op in [o for o in ops if o.next]:
+        ms = statistics.mean(op.times_ms)
+        tf = op.flops / (ms * 1e-3) / 1e12
+        next_ops[op.name] = {"flops": op.flops, "bytes": op.bytes, "ms": round(ms, 5), "tflops": round(tf, 1),
+                             "frac_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "gbs": round(op.bytes / (ms * 1e-3) / 1e9, 1), "kernel": op.kernel}
+    ops = [o for o in ops if not o.next]
     for op in ops:
         ms = statistics.mean(op.times_ms)
         gbs = op.bytes / (ms * 1e-3) / 1e9
@@ -363,6 +386,7 @@ def main():
             "storage_dtypes": "f32 and bf16 per op name; all arithmetic in f32",
             "mall_defeat": f"each op cycles >= {MALL_DEFEAT_BYTES / 1e9:.1f} GB of buffer sets",
             "per_op": per_op,
+            "next_ops": next_ops,
         },
         "roofline": {
             "bound": "hbm",

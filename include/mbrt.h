@@ -314,6 +314,20 @@ MBRT_API int mbrt_band_mask_merge(const float* stft, const void* const* masks, i
 MBRT_API int mbrt_zero_dc(void* spec, int dtype, int64_t outer, int64_t freq_bins, int64_t frames,
                  mbrt_stream_t stream);
 
+/* ---- fused attention (MFMA) ---------------------------------------------------- */
+
+/* out[bh, i, :] = sum_j softmax_j(scale * q[bh, i, :] . k[bh, j, :]) v[bh, j, :] for bf16
+ * q [BH, n_q, head_dim], k and v [BH, n_k, head_dim] (contiguous, 16-byte aligned) and
+ * out [BH, n_q, head_dim] of out_dtype (BF16/F32); scale > 0, or 0 for 1/sqrt(head_dim).
+ * f32 accumulation and softmax; the probabilities enter the second product as a pair of
+ * bf16 values (hi + lo), so the result has f32 accuracy.  head_dim 64 only.  Replaces mbr_tile::scaled_dot_product_attention
+ * (src/mbr_cuda_tile.cu:6530-6709) and the time-attention kernels
+ * (src/mbr_time_attention_cutile.cu:108-196) for every n_q / n_k, without the [BH, n, n]
+ * score tensor. */
+MBRT_API int mbrt_attention(const void* q, const void* k, const void* v, int dtype, void* out, int out_dtype,
+                            int64_t BH, int64_t n_q, int64_t n_k, int64_t head_dim, float scale,
+                            mbrt_stream_t stream);
+
 /* ---- host-side tables (CPU only, no GPU access) ----------------------------- */
 
 /* Band layout of a MelBandRoformer: the support of a Slaney-normalised mel filterbank

@@ -55,8 +55,16 @@ KERNEL_SOURCES = [
     "k_softmax.hip",
     "k_rotary.hip",
     "k_band.hip",
+    "k_attention.hip",
     "host_tables.cpp",
 ]
+
+# Per-file compiler options.  The attention kernel keeps its MFMA accumulators in ordinary
+# VGPRs (gfx950 MFMA reads and writes them directly), so the online softmax and the
+# accumulator rescale need no AGPR <-> VGPR copies.
+EXTRA_FLAGS = {
+    "k_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 TENSOR_SOURCES = [
     "hip_context.cpp",
@@ -99,7 +107,7 @@ def _objects(srcdir: Path, names: list[str], tag: str, build_dir: Path, defines:
             obj = build_dir / f"{tag}_{Path(n).stem}.o"
             # the C-ABI library exports only its MBRT_API symbols; the C++ tensor layer
             # exports its whole API
-            extra = ["-fvisibility=default"] if tag == "t" else None
+            extra = ["-fvisibility=default"] if tag == "t" else EXTRA_FLAGS.get(n)
             futs.append(ex.submit(_compile, src, obj, defines, verbose, extra))
         for f in futs:
             objs.append(f.result())

@@ -195,7 +195,7 @@ bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) 
     else if (c <= 64 && fits(32)) launch_staged<IDT, 8, 8>(a, st);
     else if (c <= 128 && fits(16)) launch_staged<IDT, 16, 8>(a, st);
     else if (c <= 128 || !MBRT_SM_STAGE_LONG) return false;
-    else if (fits(4)) {
+    else if (MBRT_SM_LONG_G == 64 && fits(4)) {
         if (c <= 256) launch_staged<IDT, 64, 4>(a, st);
         else if (c <= 512) launch_staged<IDT, 64, 8>(a, st);
         else if (c <= 832) launch_staged<IDT, 64, 13>(a, st);

@@ -52,6 +52,9 @@
 #ifndef MBRT_SM_STAGE_LONG
 #define MBRT_SM_STAGE_LONG 1  // softmax rows of 129..1024 elements through LDS when spans align
 #endif
+#ifndef MBRT_SM_LONG_G
+#define MBRT_SM_LONG_G 64  // lanes per staged row of 129..1024 elements when 4-row spans align (64 or 32)
+#endif
 #ifndef MBRT_ACT_U
 #define MBRT_ACT_U 1     // 16-byte groups per thread in the activation kernels
 #endif

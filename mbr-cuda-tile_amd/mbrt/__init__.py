@@ -314,6 +314,17 @@ def zero_dc(spec: torch.Tensor, stream=None) -> torch.Tensor:
     return spec
 
 
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor, scale: float = 0.0,
+              stream=None) -> torch.Tensor:
+    """Fused attention: q [BH, nq, 64], k, v [BH, nk, 64] bf16 -> out [BH, nq, 64] (bf16/f32)."""
+    for t in (q, k, v, out):
+        _contig(t)
+    BH, nq, D = q.shape
+    _abi.call("mbrt_attention", _p(q), _p(k), _p(v), dtype_code(q), _p(out), dtype_code(out), BH, nq, k.shape[1], D,
+              float(scale), _s(stream))
+    return out
+
+
 # ---- host-side tables -----------------------------------------------------------------------
 
 def mel_band_layout(sample_rate: float = 44100.0, n_fft: int = 2048, n_bands: int = 60, channels: int = 2):

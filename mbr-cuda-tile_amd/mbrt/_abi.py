@@ -95,6 +95,7 @@ SIGNATURES: dict[str, list] = {
     "mbrt_band_gather": [P, P, I, P, I, L, L, L, L, P],
     "mbrt_band_mask_merge": [P, C.POINTER(P), I, I, P, P, I, P, I, P, I, L, L, L, L, L, P],
     "mbrt_zero_dc": [P, I, L, L, L, P],
+    "mbrt_attention": [P, P, P, I, P, I, L, L, L, L, Fl, P],
     "mbrt_mel_band_layout": [D, I, I, I, P, L, C.POINTER(C.c_int64), P],
     "mbrt_band_csr": [P, L, L, P, P, P, P],
     "mbrt_rotary_tables": [P, P, L, L, Fl],

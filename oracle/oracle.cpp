@@ -693,4 +693,48 @@ void orc_zero_dc(void* spec, int dt, int64_t outer, int64_t bins, int64_t T) {
         for (int64_t i = 0; i < T * 2; ++i) st(spec, dt, o * bins * T * 2 + i, 0.0f);
 }
 
+// Attention (src/mbr_cuda_tile.cu:6530-6709): s_ij = scale * q_i . k_j, p = softmax_j(s),
+// out_i = sum_j p_ij v_j; scale 0 means 1 / sqrt(D).  EXACT: double throughout, one
+// rounding of the output.  FAST: float scores and sums, probabilities rounded to bf16
+// before the second product (the reference's bf16 attention), the CPU baseline's pipeline.
+void orc_attention(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
+                   int64_t nq, int64_t nk, int64_t D, float scale, int mode) {
+    const double sc = scale == 0.0f ? 1.0 / std::sqrt((double)D) : (double)scale;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int64_t r = 0; r < BH * nq; ++r) {
+        const int64_t bh = r / nq;
+        const int64_t qb = r * D, kb0 = bh * nk * D;
+        std::vector<double> s((size_t)nk);
+        std::vector<float> qf((size_t)D);
+        for (int64_t d = 0; d < D; ++d) qf[d] = ld(q, dt, qb + d);
+        double m = -INFINITY;
+        for (int64_t j = 0; j < nk; ++j) {
+            double acc = 0.0;
+            if (mode == ORC_EXACT) {
+                for (int64_t d = 0; d < D; ++d) acc += (double)qf[d] * (double)ld(k, dt, kb0 + j * D + d);
+            } else {
+                float fa = 0.0f;
+                for (int64_t d = 0; d < D; ++d) fa += qf[d] * ld(k, dt, kb0 + j * D + d);
+                acc = fa;
+            }
+            s[j] = acc * sc;
+            m = std::max(m, s[j]);
+        }
+        double l = 0.0;
+        for (int64_t j = 0; j < nk; ++j) {
+            s[j] = mode == ORC_EXACT ? std::exp(s[j] - m) : (double)std::exp((float)(s[j] - m));
+            l += s[j];
+        }
+        for (int64_t d = 0; d < D; ++d) {
+            double acc = 0.0;
+            for (int64_t j = 0; j < nk; ++j) {
+                const double p = mode == ORC_EXACT ? s[j] : (double)bf16_to_f32(f32_to_bf16((float)s[j]));
+                acc += p * (double)ld(v, dt, kb0 + j * D + d);
+            }
+            if (mode == ORC_EXACT) st(out, odt, r * D + d, acc / l);
+            else st(out, odt, r * D + d, (float)(acc / l));
+        }
+    }
+}
+
 }  // extern "C"

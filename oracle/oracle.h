@@ -86,6 +86,8 @@ void orc_band_mask_merge(const float* stft, const void* const* masks, int mdt, i
                          const int32_t* ind, const void* cnt, int cdt, void* out, int odt, int64_t B, int64_t F,
                          int64_t T, int64_t J, int64_t C, int mode);
 void orc_zero_dc(void* spec, int dt, int64_t outer, int64_t bins, int64_t T);
+void orc_attention(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
+                   int64_t nq, int64_t nk, int64_t D, float scale, int mode);
 
 #ifdef __cplusplus
 }

@@ -296,3 +296,12 @@ def zero_dc(spec, dt):
     outer, bins, T, _ = spec.shape
     lib().orc_zero_dc(_p(spec), dt, L(outer), L(bins), L(T))
     return spec
+
+
+def attention(q, k, v, dt, odt, scale=0.0, mode=EXACT):
+    """q [BH, nq, D], k and v [BH, nk, D] -> softmax(scale q k^T) v [BH, nq, D]."""
+    BH, nq, D = q.shape
+    nk = k.shape[1]
+    out = empty((BH, nq, D), odt)
+    lib().orc_attention(_p(q), _p(k), _p(v), dt, _p(out), odt, L(BH), L(nq), L(nk), L(D), C.c_float(scale), mode)
+    return out

@@ -555,3 +555,52 @@ def test_zero_dc(orc, dev):
         mbrt.zero_dc(xd)
         torch.cuda.synchronize()
         assert_bitexact(to_host(xd, dt), orc.zero_dc(x, dt), "zero_dc")
+
+
+# ---- fused attention -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("BH,nq,nk", [(3, 1, 1), (3, 5, 5), (2, 60, 60), (2, 64, 64), (2, 65, 65), (2, 130, 130),
+                                      (2, 801, 801), (2, 37, 200), (2, 200, 37)])
+@pytest.mark.parametrize("odt", [BF16, F32])
+def test_attention_shapes(orc, dev, BH, nq, nk, odt):
+    say(f"attention BH={BH} nq={nq} nk={nk} out={odt}")
+    q = inp(orc, (BH, nq, 64), 0x4D425200A0, nq, BF16)
+    k = inp(orc, (BH, nk, 64), 0x4D425200A1, nk, BF16)
+    v = inp(orc, (BH, nk, 64), 0x4D425200A2, nk, BF16)
+    out = empty((BH, nq, 64), odt)
+    mbrt.attention(to_dev(q, BF16), to_dev(k, BF16), to_dev(v, BF16), out, 0.0)
+    torch.cuda.synchronize()
+    ref = orc.attention(q, k, v, BF16, odt, 0.0)
+    # outputs are sums of p v of either sign: the magnitude they cancel from is sum p |v|
+    den = orc.attention(orc.to_f32(q, BF16), orc.to_f32(k, BF16), np.abs(orc.to_f32(v, BF16)), F32, F32, 0.0)
+    print("attention errors", assert_close(to_host(out, odt), ref, odt, "attention", den=den))
+
+
+@pytest.mark.parametrize("BH,N,scale", [(480, 801, 0.125), (6408, 60, 0.125)])
+def test_attention_full_shapes(orc, dev, BH, N, scale):
+    """Time (480 heads x 801) and frequency (6408 x 60) attention at full chunk shape; the
+    oracle checks every query of a sample of heads."""
+    say(f"attention full BH={BH} N={N}")
+    g = torch.Generator(device="cuda").manual_seed(SEED[3] + N)
+    q, k, v = (torch.randn((BH, N, 64), generator=g, device="cuda").to(torch.bfloat16) for _ in range(3))
+    out = torch.empty((BH, N, 64), dtype=torch.bfloat16, device="cuda")
+    mbrt.attention(q, k, v, out, scale)
+    torch.cuda.synchronize()
+    sel = torch.tensor(sorted(np.random.default_rng(5).choice(BH, 6, replace=False)), device="cuda")
+    qs, ks, vs = (to_host(t[sel], BF16) for t in (q, k, v))
+    ref = orc.attention(qs, ks, vs, BF16, BF16, scale)
+    den = orc.attention(orc.to_f32(qs, BF16), orc.to_f32(ks, BF16), np.abs(orc.to_f32(vs, BF16)), F32, F32, scale)
+    print("attention full errors", assert_close(to_host(out[sel], BF16), ref, BF16, "attention", den=den))
+
+
+def test_attention_rejects_bad_arguments(dev):
+    q = torch.zeros((2, 8, 32), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty_like(q)
+    with pytest.raises(mbrt.MbrtError):
+        mbrt.attention(q, q, q, out)  # head_dim 32 is not built
+    q64 = torch.zeros((2, 8, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(mbrt.MbrtError):
+        mbrt.attention(q64, q64, q64, torch.empty_like(q64))  # f32 inputs
+    qb = q64.to(torch.bfloat16)
+    with pytest.raises(mbrt.MbrtError):
+        mbrt.attention(qb, qb, qb, torch.empty_like(qb), -0.5)  # negative scale

@@ -362,3 +362,30 @@ def test_zero_dc(orc):
     x = orc.randn((3, 5, 4, 2), seed=55)
     y = orc.zero_dc(x, F32)
     assert np.all(y[:, 0] == 0) and np.array_equal(y[:, 1:], x[:, 1:])
+
+
+# ---- attention -------------------------------------------------------------------------------
+
+def test_attention_matches_numpy_and_closed_forms(orc):
+    """Double oracle vs a numpy float64 einsum formulation; equal keys give the mean of v;
+    constant v gives v; the FAST (f32, bf16-probability) pipeline stays within 5e-3."""
+    for (BH, nq, nk, scale) in [(2, 5, 7, 0.0), (3, 33, 70, 0.3), (1, 64, 64, 0.125)]:
+        q = orc.randn((BH, nq, 64), seed=11, stream=nq)
+        k = orc.randn((BH, nk, 64), seed=12, stream=nk)
+        v = orc.randn((BH, nk, 64), seed=13, stream=nk)
+        out = orc.attention(q, k, v, F32, F32, scale)
+        sc = scale or 1.0 / 8.0
+        s = np.einsum("bid,bjd->bij", q.astype(np.float64), k.astype(np.float64)) * sc
+        p = np.exp(s - s.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        ref = np.einsum("bij,bjd->bid", p, v.astype(np.float64))
+        assert np.abs(out - ref).max() < 1e-6
+        fast = orc.attention(q, k, v, F32, F32, scale, mode=orc.FAST)
+        assert np.linalg.norm(fast - ref) / np.linalg.norm(ref) < 5e-3
+    q = orc.randn((1, 4, 64), seed=14)
+    k = np.repeat(orc.randn((1, 1, 64), seed=15), 9, axis=1)
+    v = orc.randn((1, 9, 64), seed=16)
+    out = orc.attention(q, k, v, F32, F32, 0.0)
+    assert np.allclose(out, np.broadcast_to(v.mean(axis=1, keepdims=True), out.shape), atol=1e-6)
+    ones = np.ones((1, 9, 64), np.float32) * 3.0
+    assert np.allclose(orc.attention(q, orc.randn((1, 9, 64), seed=17), ones, F32, F32, 0.0), 3.0, atol=1e-6)
