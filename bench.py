@@ -349,6 +349,9 @@ def main():
                            "buffer_sets": len(op.sets), "kernel": op.kernel}
         tot_bytes += op.bytes
         tot_ms += ms
+    if not ops:  # a tuning run of next_ops only
+        print(json.dumps({"config": {"next_ops": next_ops}}), flush=True)
+        return
     dom = max(ops, key=lambda o: statistics.mean(o.times_ms))
     dom_ms = statistics.mean(dom.times_ms)
     achieved = dom.bytes / (dom_ms * 1e-3) / 1e9

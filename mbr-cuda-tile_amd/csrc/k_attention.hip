@@ -4,15 +4,18 @@
 // The [BH, N, N] score matrix never reaches HBM: each workgroup streams K/V tiles through
 // LDS and keeps an online softmax (running max m, running sum l) per query.
 //
-// Workgroup = 4 waves = 64 queries of one (b, h); wave w owns queries q0 .. q0+15.
+// Workgroup = 4 waves of one (b, h); wave w owns 16 or 32 queries (QS sub-blocks of 16).
 // Per 64-key tile, with v_mfma_f32_16x16x32_bf16 (lane l: A[l%16][8(l/16)+j],
 // B[8(l/16)+j][l%16], C[4(l/16)+i][l%16]):
 //   S^T = K Q^T     8 MFMAs: A = K rows from LDS, B = the wave's Q fragment (registers).
 //                   Lane l then holds S^T[key 16kb + 4(l/16) + i][query l%16].
 //   online softmax  per query l%16: max/sum over the lane's 16 keys, then over the four
-//                   lane groups (xor 16, xor 32); the accumulator is rescaled in place.
+//                   lane groups (xor 16, xor 32); the accumulator is rescaled in place
+//                   only when the max outgrows the exponent reference by 2^8.
 //   O^T += V^T P^T  16 MFMAs: B = P^T straight from the S^T registers, as a bf16 pair
-//                   P_hi + P_lo; A = V^T from a transposed LDS copy of the V tile.  The contraction runs over
+//                   P_hi + P_lo; A = V^T read from the row-major V tile with the gfx950
+//                   LDS transpose read (ds_read_b64_tr_b16).
+//   (MFMA counts per 16-query sub-block.)  The contraction runs over
 //                   keys in the order the S^T layout holds them (slot j of lane group g is
 //                   key 4g+j for j < 4, 16+4g+(j-4) after), used for both operands.
 //   Lane l accumulates O^T[d 16db + 4(l/16) + i][query l%16]: the softmax statistics and
@@ -33,11 +36,19 @@ constexpr int kKeys = 64;      // keys per tile
 constexpr int kQWave = 16;     // queries per wave
 constexpr int kWaves = 4;
 constexpr int kQBlock = kQWave * kWaves;
-constexpr int kPad = 8;        // LDS row padding (bf16 elements)
+constexpr float kLazy = 8.0f;  // log2 units the running max may outgrow the exponent reference
+#ifndef MBRT_ATTN_PAD
+#define MBRT_ATTN_PAD 8
+#endif
+constexpr int kPad = MBRT_ATTN_PAD;  // LDS row padding (bf16 elements)
+#ifndef MBRT_ATTN_QS2_MIN
+#define MBRT_ATTN_QS2_MIN 1  // 32 queries per wave when n_q exceeds this many 64-query blocks
+#endif
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;  // an LDS-resident bf16x4
 
 struct AttnArgs {
     const __bf16* q;
@@ -58,40 +69,50 @@ __device__ __forceinline__ float xor_sum(float x) {
     return x + __shfl_xor(x, 32);
 }
 
-template <int ODT>
+// QS = 16-query sub-blocks per wave (1 or 2): every K and V^T fragment read from LDS
+// feeds QS MFMAs, so longer sequences use QS = 2 (128 queries per workgroup).
+template <int ODT, int QS>
 __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) __bf16 ks[kKeys][kHeadDim + kPad];   // K tile [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 vts[kHeadDim][kKeys + kPad];  // V tile transposed [d][key]
+    __shared__ __attribute__((aligned(16))) __bf16 vs[kKeys][kHeadDim + kPad];   // V tile [key][d]
+    constexpr int kQB = kQWave * QS * kWaves;  // queries per workgroup
     const int tid = threadIdx.x;
     const int lane = tid % 64, g = lane / 16, c = lane % 16;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
     // one linear grid, query tiles of one (b, h) adjacent so that they share its K/V in L2
     const int64_t bh = blockIdx.x / a.qtiles;
-    const int q0 = (blockIdx.x % a.qtiles) * kQBlock + w * kQWave;
+    const int q0 = (blockIdx.x % a.qtiles) * kQB + w * kQWave * QS;
     const __bf16* kbase = a.k + bh * a.nk * kHeadDim;
     const __bf16* vbase = a.v + bh * a.nk * kHeadDim;
 
-    // Q fragment: lane holds Q[q0 + c][32s + 8g .. +7] for s = 0, 1
-    const __bf16* qrow = a.q + (bh * a.nq + min(q0 + c, a.nq - 1)) * kHeadDim;
-    bf16x8 qf[2];
+    // Q fragments: for sub-block x, lane holds Q[q0 + 16x + c][32s + 8g .. +7], s = 0, 1
+    bf16x8 qf[QS][2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
+    for (int x = 0; x < QS; ++x) {
+        const __bf16* qrow = a.q + (bh * a.nq + min(q0 + 16 * x + c, a.nq - 1)) * kHeadDim;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) qf[x][s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
+    }
 
-    f32x4 o[4];
+    f32x4 o[QS][4];
+    float m[QS], l[QS];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m = -INFINITY, l = 0.0f;
+    for (int x = 0; x < QS; ++x) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[x][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        m[x] = -INFINITY;
+        l[x] = 0.0f;
+    }
 
     // K/V tiles: 64 keys x 64 d = 512 16-byte vectors each, 2 per thread.  The next tile
     // is fetched into registers while the current one is computed from LDS.
-    // Lane l of wave w stages key l, d chunks 8 (w + 4u): the transposed V writes of one
-    // instruction then fill one LDS row with 64 consecutive keys.
+    // Thread t stages the 16-byte vectors t and t + 256 (key = vector / 8) of each tile.
     bf16x8 kv[2], vv[2];
     auto fetch = [&](int kt) {
-        const int64_t row = min(kt + lane, a.nk - 1);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int dc = 8 * (w + 4 * u);
+            const int vec = tid + 256 * u, dc = (vec & 7) * 8;
+            const int64_t row = min(kt + (vec >> 3), a.nk - 1);
             kv[u] = *reinterpret_cast<const bf16x8*>(kbase + row * kHeadDim + dc);
             vv[u] = *reinterpret_cast<const bf16x8*>(vbase + row * kHeadDim + dc);
         }
@@ -101,100 +122,127 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs a) {
         __syncthreads();  // the previous tile is no longer read
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int dc = 8 * (w + 4 * u);
-            *reinterpret_cast<bf16x8*>(&ks[lane][dc]) = kv[u];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) vts[dc + j][lane] = vv[u][j];
+            const int vec = tid + 256 * u, key = vec >> 3, dc = (vec & 7) * 8;
+            *reinterpret_cast<bf16x8*>(&ks[key][dc]) = kv[u];
+            *reinterpret_cast<bf16x8*>(&vs[key][dc]) = vv[u];
         }
         __syncthreads();
         if (kt + kKeys < a.nk) fetch(kt + kKeys);
 
-        // S^T = K Q^T for the 4 key blocks of the tile
-        f32x4 st[4];
+        // S^T = K Q^T for the 4 key blocks of the tile and every query sub-block
+        f32x4 st[QS][4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            st[kb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int x = 0; x < QS; ++x) st[x][kb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&ks[16 * kb + c][32 * s + 8 * g]);
-                st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[s], st[kb], 0, 0, 0);
+#pragma unroll
+                for (int x = 0; x < QS; ++x)
+                    st[x][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[x][s], st[x][kb], 0, 0, 0);
             }
         }
-        // online softmax over this tile, per query c, on raw scores: the scale is folded
-        // into the exponent, exp2(scale log2e (s - max)); keys past N only in the last tile
+        // online softmax per query, on raw scores: the scale is folded into the exponent,
+        // exp2(scale log2e (s - max)); keys past N occur only in the last tile
         if (kt + kKeys > a.nk) {
 #pragma unroll
+            for (int x = 0; x < QS; ++x)
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (kt + 16 * kb + 4 * g + i >= a.nk) st[x][kb][i] = -INFINITY;
+        }
+#pragma unroll
+        for (int x = 0; x < QS; ++x) {
+            // m[x] is the exponent reference in log2 units.  It moves only when the tile's
+            // scaled max exceeds it by more than kLazy: P <= 2^kLazy then, harmless in f32
+            // and in the bf16 pair, and the accumulator is rescaled about once per query.
+            float mx = -INFINITY;
+#pragma unroll
             for (int kb = 0; kb < 4; ++kb)
+                mx = fmaxf(mx, fmaxf(fmaxf(st[x][kb][0], st[x][kb][1]), fmaxf(st[x][kb][2], st[x][kb][3])));
+            mx = xor_max(mx) * a.scale_log2e;
+            if (mx > m[x] + kLazy) {
+                const float alpha = __builtin_amdgcn_exp2f(m[x] - mx);
+                l[x] *= alpha;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (kt + 16 * kb + 4 * g + i >= a.nk) st[kb][i] = -INFINITY;
-        }
-        float mx = m;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-            mx = fmaxf(mx, fmaxf(fmaxf(st[kb][0], st[kb][1]), fmaxf(st[kb][2], st[kb][3])));
-        mx = xor_max(mx);
-        const float mxs = mx * a.scale_log2e;
-        float psum = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(st[kb][i], a.scale_log2e, -mxs));
-                st[kb][i] = p;
-                psum += p;
+                for (int db = 0; db < 4; ++db) o[x][db] *= alpha;
+                m[x] = mx;
             }
-        }
-        psum = xor_sum(psum);
-        if (mx != m) {  // the accumulator keeps its scale until some running max moves
-            const float alpha = __builtin_amdgcn_exp2f((m - mx) * a.scale_log2e);
-            l *= alpha;
+            float psum = 0.0f;
 #pragma unroll
-            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(st[x][kb][i], a.scale_log2e, -m[x]));
+                    st[x][kb][i] = p;
+                    psum += p;
+                }
+            }
+            l[x] += xor_sum(psum);
         }
-        l += psum;
-        m = mx;
 
-        // O^T += V^T P^T over the two 32-key chunks
+        // O^T += V^T P^T over the two 32-key chunks.  P = P_hi + P_lo, both bf16: hi is P
+        // truncated to bf16 (exact), lo = P - hi (exact in f32) rounded to bf16, so the
+        // pair carries 16 mantissa bits and the product keeps f32 accuracy.
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            // P = P_hi + P_lo, both bf16: the pair carries 16 mantissa bits of P, so the
-            // second product loses nothing measurable to the bf16 operand format
-            bf16x8 ph, pl;
+            bf16x8 ph[QS], pl[QS];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p0 = st[2 * cc][i], p1 = st[2 * cc + 1][i];
-                ph[i] = (__bf16)p0;
-                ph[4 + i] = (__bf16)p1;
-                pl[i] = (__bf16)(p0 - (float)ph[i]);
-                pl[4 + i] = (__bf16)(p1 - (float)ph[4 + i]);
+            for (int x = 0; x < QS; ++x) {
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                    for (int i = 0; i < 4; i += 2) {
+                        const float p0 = st[x][2 * cc + h][i], p1 = st[x][2 * cc + h][i + 1];
+                        const uint32_t b0 = __float_as_uint(p0) & 0xffff0000u;
+                        const uint32_t b1 = __float_as_uint(p1) & 0xffff0000u;
+                        hw[2 * h + i / 2] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+                        lw[2 * h + i / 2] = pack_bf16x2(p0 - __uint_as_float(b0), p1 - __uint_as_float(b1));
+                    }
+                }
+                ph[x] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+                pl[x] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
             }
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const __bf16* vr = &vts[16 * db + c][32 * cc + 4 * g];
-                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
-                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 16);
+                // V^T operand by LDS transpose reads: in each 16-lane group, lane i receives
+                // element i%4 of the 8-byte chunks of lanes 4r + i/4 (r = 0..3), so lane
+                // (g, c) supplies V[32cc + 4g + c/4 (+16)][16db + 4(c%4) ..] and receives
+                // V[32cc + 4g + r (+16)][16db + c] for r = 0..3: slots j and 4 + j.
+                const int vrow = 32 * cc + 4 * g + (c >> 2), vcol = 16 * db + 4 * (c & 3);
+                const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(&vs[vrow][vcol]));
+                const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(&vs[vrow + 16][vcol]));
                 const bf16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, o[db], 0, 0, 0);
+#pragma unroll
+                for (int x = 0; x < QS; ++x) {
+                    o[x][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[x], o[x][db], 0, 0, 0);
+                    o[x][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[x], o[x][db], 0, 0, 0);
+                }
             }
         }
     }
 
-    const int q = q0 + c;
-    if (q >= a.nq) return;
-    const float inv = 1.0f / l;
-    const int64_t obase = (bh * a.nq + q) * kHeadDim;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-        const int d = 16 * db + 4 * g;
-        if constexpr (ODT == F32) {
-            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + obase + d) = o[db] * inv;
-        } else {
-            u32x2 pk;
-            pk.x = pack_bf16x2(o[db][0] * inv, o[db][1] * inv);
-            pk.y = pack_bf16x2(o[db][2] * inv, o[db][3] * inv);
-            *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + obase + d) = pk;
+    for (int x = 0; x < QS; ++x) {
+        const int q = q0 + 16 * x + c;
+        if (q >= a.nq) continue;
+        const float inv = 1.0f / l[x];
+        const int64_t obase = (bh * a.nq + q) * kHeadDim;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 16 * db + 4 * g;
+            if constexpr (ODT == F32) {
+                *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + obase + d) = o[x][db] * inv;
+            } else {
+                u32x2 pk;
+                pk.x = pack_bf16x2(o[x][db][0] * inv, o[x][db][1] * inv);
+                pk.y = pack_bf16x2(o[x][db][2] * inv, o[x][db][3] * inv);
+                *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + obase + d) = pk;
+            }
         }
     }
 }
@@ -229,10 +277,18 @@ int mbrt_attention(const void* q, const void* k, const void* v, int dtype, void*
     a.nq = (int)n_q;
     a.nk = (int)n_k;
     a.scale_log2e = (scale == 0.0f ? 1.0f / std::sqrt((float)head_dim) : scale) * 1.44269504088896340736f;
-    a.qtiles = (uint32_t)ceil_div(n_q, kQBlock);
+    // two query sub-blocks per wave once a (b, h) has more than one workgroup of queries
+    const int qs = n_q > kQBlock * MBRT_ATTN_QS2_MIN ? 2 : 1;
+    a.qtiles = (uint32_t)ceil_div(n_q, (int64_t)kQBlock * qs);
     const dim3 grid((unsigned)(BH * a.qtiles));
-    if (out_dtype == BF16) hipLaunchKernelGGL(attention_kernel<BF16>, grid, dim3(kWaves * 64), 0, as_stream(stream), a);
-    else hipLaunchKernelGGL(attention_kernel<F32>, grid, dim3(kWaves * 64), 0, as_stream(stream), a);
+    hipStream_t st = as_stream(stream);
+    if (qs == 2) {
+        if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 2>), grid, dim3(kWaves * 64), 0, st, a);
+        else hipLaunchKernelGGL((attention_kernel<F32, 2>), grid, dim3(kWaves * 64), 0, st, a);
+    } else {
+        if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 1>), grid, dim3(kWaves * 64), 0, st, a);
+        else hipLaunchKernelGGL((attention_kernel<F32, 1>), grid, dim3(kWaves * 64), 0, st, a);
+    }
     return check_launch(op);
 }
 
