@@ -105,8 +105,9 @@ def build_ops(torch, mbrt, bands):
     # BL-2c sigmoid gate x head merge bf16, attention output head-major [B, H, N, D]
     B, H, N, Dh = 60, 8, 801, 64
     op = Op("bl2c_gate_merge_bf16", 2 * B * H * N * Dh * 2 + B * N * H * 2,
-            lambda: dict(a=randn((B, H, N, Dh), bf16), gl=randn((B, N, H), bf16, 2.0),
-                         y=torch.empty((B, N, H * Dh), dtype=bf16, device=dev)), "gate_merge_vec_kernel")
+            lambda B=B, H=H, N=N, Dh=Dh: dict(a=randn((B, H, N, Dh), bf16), gl=randn((B, N, H), bf16, 2.0),
+                                              y=torch.empty((B, N, H * Dh), dtype=bf16, device=dev)),
+            "gate_merge_vec_kernel")
     op.run = lambda b: mbrt.gate_merge(b["a"], b["gl"], b["y"], mbrt.LAYOUT_BHND)
     ops.append(op)
 
@@ -159,12 +160,13 @@ def build_ops(torch, mbrt, bands):
     # Fused attention (MFMA), the first widening beyond the tensor-op path: q, k, v bf16
     # [BH, N, 64] for the time (480 x 801) and frequency (6408 x 60) attention.  Reported in
     # config.next_ops with TFLOP/s (4 BH N^2 64 flop); not part of `value`.
-    for tag, BH, N in (("time", 480, 801), ("freq", 6408, 60)):
-        op = Op(f"attention_{tag}_bf16", 4 * BH * N * 64 * 2,
-                (lambda BH=BH, N=N: dict(q=randn((BH, N, 64), bf16), k=randn((BH, N, 64), bf16),
-                                         v=randn((BH, N, 64), bf16), y=torch.empty((BH, N, 64), dtype=bf16, device=dev))),
+    for atag, abh, an in (("time", 480, 801), ("freq", 6408, 60)):
+        op = Op(f"attention_{atag}_bf16", 4 * abh * an * 64 * 2,
+                (lambda abh=abh, an=an: dict(q=randn((abh, an, 64), bf16), k=randn((abh, an, 64), bf16),
+                                             v=randn((abh, an, 64), bf16),
+                                             y=torch.empty((abh, an, 64), dtype=bf16, device=dev))),
                 "attention_kernel")
-        op.flops = 4.0 * BH * N * N * 64
+        op.flops = 4.0 * abh * an * an * 64
         op.next = True
         op.run = lambda b: mbrt.attention(b["q"], b["k"], b["v"], b["y"], 0.125)
         ops.append(op)
@@ -347,6 +349,9 @@ def main():
         per_op[op.name] = {"bytes": op.bytes, "ms": round(ms, 5), "median_ms": round(statistics.median(op.times_ms), 5),
                            "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                            "buffer_sets": len(op.sets), "kernel": op.kernel}
+        if gbs > HBM_PEAK_GBS:  # inputs are cycled past the MALL: this can only be a measurement error
+            print(f"bench.py: {op.name} reports {gbs:.0f} GB/s, above the HBM peak", file=sys.stderr)
+            per_op[op.name]["suspect"] = True
         tot_bytes += op.bytes
         tot_ms += ms
     if not ops:  # a tuning run of next_ops only

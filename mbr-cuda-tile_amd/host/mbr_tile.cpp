@@ -192,6 +192,23 @@ Tensor apply_gate_logits_and_merge_heads(const Tensor& attn, const Tensor& gate_
     return gate_merge(attn, gate_logits, heads, dim_head, true, "mbr_tile::apply_gate_logits_and_merge_heads");
 }
 
+Tensor scaled_dot_product_attention(const Tensor& q, const Tensor& k, const Tensor& v, float scale) {
+    const char* op = "mbr_tile::scaled_dot_product_attention";
+    if (q.ndim() != 4 || k.ndim() != 4 || v.ndim() != 4 || k.shape() != v.shape() || q.size(0) != k.size(0) ||
+        q.size(1) != k.size(1) || q.size(3) != k.size(3))
+        throw std::runtime_error(std::string(op) + ": expected q [B, H, N, D] and k, v [B, H, N_k, D]");
+    auto bf16 = [](const Tensor& t) { return t.dtype() == DType::BFloat16 ? t.contiguous() : t.to_bf16().contiguous(); };
+    const Tensor qb = bf16(q), kb = bf16(k), vb = bf16(v);
+    const int64_t B = q.size(0), H = q.size(1), N = q.size(2), Nk = k.size(2), D = q.size(3);
+    const DType odt = g_quantize_bf16 ? DType::BFloat16 : DType::Float32;
+    Tensor out = Tensor::empty({B, H, N, D}, odt);
+    if (out.numel() == 0) return out;
+    abi_check(mbrt_attention(qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), MBRT_BF16, out.data_ptr(), code(odt), B * H, N,
+                             Nk, D, scale, abi_stream()),
+              op);
+    return out;
+}
+
 Tensor softmax_last_dim(const Tensor& x, float scale, DType out_dtype) {
     const Tensor xc = float_contig(x, "mbr_tile::softmax_last_dim");
     Tensor out = Tensor::empty(xc.shape(), out_dtype);

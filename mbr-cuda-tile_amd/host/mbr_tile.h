@@ -50,6 +50,12 @@ Tensor apply_gates_and_merge_heads(const Tensor& attn, const Tensor& gates, int 
 // the merge in one pass).
 Tensor apply_gate_logits_and_merge_heads(const Tensor& attn, const Tensor& gate_logits, int heads, int dim_head);
 
+// softmax(scale q k^T) v for q [B, H, N, D], k and v [B, H, N_k, D] with D = 64, fused on
+// MFMA without the [B*H, N, N_k] score tensor (src/mbr_cuda_tile.cu:6530-6709); scale 0
+// means 1/sqrt(D).  Inputs that are not bf16 are converted to bf16 first; the result is
+// BF16 under g_quantize_bf16, else F32.
+Tensor scaled_dot_product_attention(const Tensor& q, const Tensor& k, const Tensor& v, float scale);
+
 // Row softmax of attention scores over the last dim, p = softmax(scale * x), f32
 // accumulation (the scale_softmax kernels, src/mbr_cuda_tile.cu:5092-5285).
 Tensor softmax_last_dim(const Tensor& x, float scale, DType out_dtype);

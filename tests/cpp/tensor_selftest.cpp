@@ -304,6 +304,11 @@ void ops(const std::string& path) {
     M::apply_rotary_time_split_contig_inplace(q, k, I["cos"], I["sin"]);
     d.save("rot_q", q);
     d.save("rot_k", k);
+    {
+        Tensor qa = I["q"].permute({0, 2, 1, 3}).contiguous();  // [B, H, N, D]
+        Tensor ka = I["k"].permute({0, 2, 1, 3}).contiguous();
+        d.save("attention", M::scaled_dot_product_attention(qa, ka, ka, 0.0f));
+    }
     Tensor sq, sk, sv;
     M::split_qkv_heads_rotary(I["qkv"], 8, 64, I["cos"], I["sin"], sq, sk, sv);
     d.save("split_q", sq);

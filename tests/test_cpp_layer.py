@@ -53,7 +53,8 @@ API = [
     "cudasep::mbr_tile::glu_last_dim(", "cudasep::mbr_tile::tanh_act(", "cudasep::mbr_tile::zero_dc(",
     "cudasep::mbr_tile::residual_bf16_enabled(", "cudasep::mbr_tile::bias_bf16_enabled(",
     "cudasep::mbr_tile::norm_gamma_bf16_enabled(", "cudasep::mbr_tile::bands_per_freq_bf16_enabled(",
-    "cudasep::mbr_tile::rotary_freqs_bf16_enabled(", "cudasep::HipMemoryPool::allocate(",
+    "cudasep::mbr_tile::rotary_freqs_bf16_enabled(", "cudasep::mbr_tile::scaled_dot_product_attention(",
+    "cudasep::HipMemoryPool::allocate(",
     "cudasep::HipMemoryPool::deallocate(", "cudasep::HipMemoryPool::trim_cached_memory(",
 ]
 
@@ -179,6 +180,14 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
     rq, rk = orc.rotary(q, k, BF16, cos, sin, F32, N, H, layout=1)
     assert_close(_read(tmp_path, "rot_q")[1], rq, BF16, "rotary q")
     assert_close(_read(tmp_path, "rot_k")[1], rk, BF16, "rotary k")
+    qa = np.ascontiguousarray(q.reshape(B, N, H, Dh).transpose(0, 2, 1, 3)).reshape(B * H, N, Dh)
+    ka = np.ascontiguousarray(k.reshape(B, N, H, Dh).transpose(0, 2, 1, 3)).reshape(B * H, N, Dh)
+    dt, y = _read(tmp_path, "attention")
+    assert dt == BF16 and y.shape == (B, H, N, Dh)
+    ref = orc.attention(qa, ka, ka, BF16, BF16, 0.0).reshape(B, H, N, Dh)
+    den = orc.attention(orc.to_f32(qa, BF16), orc.to_f32(ka, BF16), np.abs(orc.to_f32(ka, BF16)), F32, F32,
+                        0.0).reshape(B, H, N, Dh)
+    assert_close(y, ref, BF16, "scaled_dot_product_attention", den=den)
     sq, sk, sv = orc.split_qkv(qkv, BF16, cos, sin, F32, BF16, B, N, H, Dh, 64)
     for name, ref in (("split_q", sq), ("split_k", sk), ("split_v", sv)):
         dt, y = _read(tmp_path, name)
