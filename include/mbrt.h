@@ -328,6 +328,48 @@ MBRT_API int mbrt_attention(const void* q, const void* k, const void* v, int dty
                             int64_t BH, int64_t n_q, int64_t n_k, int64_t head_dim, float scale,
                             mbrt_stream_t stream);
 
+/* ---- STFT / iSTFT (n_fft = win_length = 2048) --------------------------------- */
+
+/* Hann window of `size` f32 samples, 0.5 (1 - cos(2 pi n / size)) in f32; size 1 gives
+ * [1].  Replaces stft_tile::hann_window (src/stft_cuda_tile.cu:514-528). */
+MBRT_API int mbrt_hann_window(float* out, int64_t size, mbrt_stream_t stream);
+
+/* Frames of an STFT: padded = length + 2048 when centred, else length;
+ * T = (padded - 2048) / hop + 1 (src/stft_cuda_tile.cu:544-551).  0 when padded < 2048,
+ * -1 for a negative length or hop < 1.  Host only. */
+MBRT_API int64_t mbrt_stft_num_frames(int64_t length, int64_t hop, int center);
+
+/* STFT of `batch` f32 signals [batch, length] with a 2048-sample f32 window:
+ * out[b, f, t] (complex, [batch, 1025, T, 2] f32) = sum_n x_pad[b, t hop + n] w[n]
+ * exp(-2 pi i f n / 2048), x_pad = x reflect-padded by 1024 on both sides when centred
+ * (reflect once about the end samples, then clamp, as Tensor::pad_reflect), times
+ * 1/sqrt(2048) when normalized.  Requires n_fft = win_length = window_numel = 2048 and
+ * T >= 1 (the reference reads past a non-centred signal shorter than 2048; this is an
+ * MBRT_E_SHAPE error here).  Replaces stft_tile::stft (src/stft_cuda_tile.cu:530-598). */
+MBRT_API int mbrt_stft(const float* signal, const float* window, float* out, int64_t batch, int64_t length,
+                       int64_t n_fft, int64_t hop, int64_t win_length, int64_t window_numel, int center,
+                       int normalized, mbrt_stream_t stream);
+
+/* Output length of mbrt_istft: `length` when > 0, else 2048 + (frames - 1) hop, minus 2048
+ * when centred.  -1 for frames < 1 or hop < 1.  Host only. */
+MBRT_API int64_t mbrt_istft_output_length(int64_t frames, int64_t hop, int center, int64_t length);
+
+/* Workspace mbrt_istft needs: batch * frames * 2048 f32 (the windowed frames). */
+MBRT_API int64_t mbrt_istft_workspace_bytes(int64_t batch, int64_t frames);
+
+/* Inverse STFT of spec [batch, 1025, frames, 2] (F32 or BF16; times sqrt(2048) when
+ * normalized): each frame is the real inverse DFT (imaginary parts of bins 0 and 1024
+ * ignored) times the window, overlap-added at hop spacing and divided by the window's
+ * summed squares where that sum exceeds 1e-8; centred output drops 1024 samples at each
+ * end; `length` > 0 trims or zero-fills to that length.  out is [batch,
+ * mbrt_istft_output_length(...)] f32.  Frames are summed per sample in frame order (the
+ * reference adds them with atomics).  Replaces stft_tile::istft
+ * (src/stft_cuda_tile.cu:600-717). */
+MBRT_API int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out, int64_t batch,
+                        int64_t freq_bins, int64_t frames, int64_t n_fft, int64_t hop, int64_t win_length,
+                        int64_t window_numel, int center, int normalized, int64_t length, void* workspace,
+                        int64_t workspace_bytes, mbrt_stream_t stream);
+
 /* ---- host-side tables (CPU only, no GPU access) ----------------------------- */
 
 /* Band layout of a MelBandRoformer: the support of a Slaney-normalised mel filterbank

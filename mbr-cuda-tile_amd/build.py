@@ -56,6 +56,7 @@ KERNEL_SOURCES = [
     "k_rotary.hip",
     "k_band.hip",
     "k_attention.hip",
+    "k_stft.hip",
     "host_tables.cpp",
 ]
 
@@ -72,6 +73,7 @@ TENSOR_SOURCES = [
     "tensor.cpp",
     "tensor_tile.cpp",
     "mbr_tile.cpp",
+    "stft_tile.cpp",
 ]
 
 

@@ -1,0 +1,551 @@
+// STFT and iSTFT for n_fft = win_length = 2048 (src/stft_cuda_tile.cu:530-717): the
+// spectrogram producer in front of the band gather and the waveform consumer after the
+// mask merge, in the layouts those ops use ([B, 1025, T, 2] f32 spectra).
+//
+// The 2048-point real transform is a 1024-point complex FFT of z[m] = x[2m] + i x[2m+1]
+// with the standard real-input split X[f] = (Z[f] + Z*[1024-f])/2 - i W^f (Z[f] -
+// Z*[1024-f])/2 (W = exp(-2 pi i / 2048)), and the inverse split for the iSTFT.
+// One wave transforms one frame; lane l holds z[l + 64a], a = 0..15, in registers.  The
+// 1024-point FFT runs as three Stockham passes, radix 16 (in registers), 16 and 4, with
+// two exchanges through the frame's LDS slot (index p stored at p + p/16, which keeps
+// both the strided and the contiguous access patterns free of bank conflicts).
+//
+// Workgroup = 4 waves, kTF consecutive frames (flattened over batch x time).  The frames'
+// spectra stay in LDS so that the [B, F, T] layout is written (STFT) or read (iSTFT) as
+// runs of kTF consecutive frames per bin, instead of one 8-byte element per 8*T bytes.
+//
+// STFT   one kernel: reflect-padded frame load with the window applied, FFT, real split,
+//        optional 1/sqrt(2048), transposed store.
+// iSTFT  two kernels: (1) transposed spectrum load (f32 or bf16, times sqrt(2048) when
+//        normalized), inverse split, inverse FFT, window and 1/2048, frames to a caller
+//        workspace [B*T, 2048]; (2) overlap-add as a gather: each output sample sums the
+//        <= ceil(2048/hop) frames that cover it in frame order and divides by the window
+//        sum of squares where that exceeds 1e-8; centre trim and the `length` trim / zero
+//        fill are part of the same pass.  No atomics: the result is deterministic.
+#include "abi_common.hpp"
+
+#include <cmath>
+
+namespace mbrt {
+namespace {
+
+constexpr int kN = 2048;        // n_fft = win_length
+constexpr int kBins = kN / 2 + 1;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+#ifndef MBRT_STFT_TF
+#define MBRT_STFT_TF 8
+#endif
+constexpr int kTF = MBRT_STFT_TF;  // frames per workgroup
+// LDS slot of one frame, in complex elements: holds padded indices up to pad(1024) = 1088;
+// 1092 complex = 2184 words = 8 (mod 64) words, so the transposed pass (kTF lanes of one
+// bin reading kTF slots) spreads over all banks.
+constexpr int kSlot = 1092;
+static_assert(kTF >= 1 && kTF <= 16 && (kThreads % kTF) == 0, "frames per workgroup");
+
+__device__ __forceinline__ int pad16(int p) { return p + (p >> 4); }
+
+// ---- twiddles W^i = exp(-2 pi i i / 2048), built at compile time -----------------------
+// cos/sin on [0, pi/4] by their Taylor series in double, extended to the circle by the
+// octant symmetries, then rounded once to f32.
+struct TwiddleTable {
+    float v[2 * kN];  // (re, im) pairs
+};
+
+constexpr void taylor_cos_sin(double x, double& c, double& s) {
+    double tc = 1.0, ts = x;
+    const double x2 = x * x;
+    c = 0.0;
+    s = 0.0;
+    for (int k = 0; k < 16; ++k) {
+        c += tc;
+        s += ts;
+        tc *= -x2 / (double)((2 * k + 1) * (2 * k + 2));
+        ts *= -x2 / (double)((2 * k + 2) * (2 * k + 3));
+    }
+}
+
+constexpr TwiddleTable make_twiddles() {
+    TwiddleTable t{};
+    constexpr double kPi = 3.14159265358979323846;
+    for (int i = 0; i < kN; ++i) {
+        const int quarter = i / 512, j = i % 512;
+        double c = 0.0, s = 0.0;
+        if (j <= 256) {
+            taylor_cos_sin(kPi * j / 1024.0, c, s);
+        } else {
+            double c2 = 0.0, s2 = 0.0;
+            taylor_cos_sin(kPi * (512 - j) / 1024.0, c2, s2);
+            c = s2;
+            s = c2;
+        }
+        double cc = c, ss = s;  // cos, sin of quarter * pi/2 + theta
+        if (quarter == 1) { cc = -s; ss = c; }
+        if (quarter == 2) { cc = -c; ss = -s; }
+        if (quarter == 3) { cc = s; ss = -c; }
+        t.v[2 * i] = (float)cc;
+        t.v[2 * i + 1] = (float)(-ss);
+    }
+    return t;
+}
+
+__constant__ const TwiddleTable kTwiddles = make_twiddles();
+
+struct cf {
+    float x, y;
+};
+__device__ __forceinline__ cf cadd(cf a, cf b) { return {a.x + b.x, a.y + b.y}; }
+__device__ __forceinline__ cf csub(cf a, cf b) { return {a.x - b.x, a.y - b.y}; }
+__device__ __forceinline__ cf cmul(cf a, cf b) { return {a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x}; }
+// times -i (forward) or +i (inverse)
+template <bool INV>
+__device__ __forceinline__ cf rot(cf a) {
+    return INV ? cf{-a.y, a.x} : cf{a.y, -a.x};
+}
+// W^i (forward) or its conjugate (inverse), 0 <= i < 2048
+template <bool INV>
+__device__ __forceinline__ cf twiddle(int i) {
+    const float2 w = reinterpret_cast<const float2*>(kTwiddles.v)[i];
+    return INV ? cf{w.x, -w.y} : cf{w.x, w.y};
+}
+
+template <bool INV>
+__device__ __forceinline__ void dft4(cf& a0, cf& a1, cf& a2, cf& a3) {
+    const cf t0 = cadd(a0, a2), t1 = csub(a0, a2), t2 = cadd(a1, a3), t3 = rot<INV>(csub(a1, a3));
+    a0 = cadd(t0, t2);
+    a2 = csub(t0, t2);
+    a1 = cadd(t1, t3);
+    a3 = csub(t1, t3);
+}
+
+// a * W16^E (conjugated for the inverse)
+template <bool INV, int E>
+__device__ __forceinline__ cf mul_w16(cf a) {
+    constexpr float C1 = 0.92387953251128675613f, S1 = 0.38268343236508977173f, H = 0.70710678118654752440f;
+    if constexpr (E == 4) return rot<INV>(a);
+    constexpr float re = E == 1 ? C1 : E == 2 ? H : E == 3 ? S1 : E == 6 ? -H : -C1;  // E = 9
+    constexpr float im = E == 1 ? -S1 : E == 2 ? -H : E == 3 ? -C1 : E == 6 ? -H : S1;
+    return cmul(a, cf{re, INV ? -im : im});
+}
+
+// 16-point DFT in place: v[r] <- sum_q v[q] W16^(q r)  (radix 4 x 4)
+template <bool INV>
+__device__ __forceinline__ void dft16(cf (&v)[16]) {
+#pragma unroll
+    for (int q0 = 0; q0 < 4; ++q0) dft4<INV>(v[q0], v[q0 + 4], v[q0 + 8], v[q0 + 12]);
+    // v[q0 + 4 r0] now holds A[q0][r0]; twiddle by W16^(q0 r0)
+    v[5] = mul_w16<INV, 1>(v[5]);
+    v[9] = mul_w16<INV, 2>(v[9]);
+    v[13] = mul_w16<INV, 3>(v[13]);
+    v[6] = mul_w16<INV, 2>(v[6]);
+    v[10] = mul_w16<INV, 4>(v[10]);
+    v[14] = mul_w16<INV, 6>(v[14]);
+    v[7] = mul_w16<INV, 3>(v[7]);
+    v[11] = mul_w16<INV, 6>(v[11]);
+    v[15] = mul_w16<INV, 9>(v[15]);
+    // DFT over q0 for each r0: inputs v[4 r0 + q0], outputs V[r0 + 4 r1]
+    cf o[16];
+#pragma unroll
+    for (int r0 = 0; r0 < 4; ++r0) {
+        cf a0 = v[4 * r0], a1 = v[4 * r0 + 1], a2 = v[4 * r0 + 2], a3 = v[4 * r0 + 3];
+        dft4<INV>(a0, a1, a2, a3);
+        o[r0] = a0;
+        o[r0 + 4] = a1;
+        o[r0 + 8] = a2;
+        o[r0 + 12] = a3;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = o[r];
+}
+
+// Orders this wave's LDS accesses: lanes of one wave exchange data through the slot.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ cf lds_ld(const float2* s, int i) {
+    const float2 t = s[i];
+    return {t.x, t.y};
+}
+__device__ __forceinline__ void lds_st(float2* s, int i, cf v) { s[i] = make_float2(v.x, v.y); }
+
+// 1024-point FFT of one frame by one wave.  In: lane l holds z[l + 64a] in v[a].  Out: lane
+// l holds Z[l + 64a] in v[a].  The slot is scratch (previous contents are overwritten).
+template <bool INV>
+__device__ __forceinline__ void fft1024(cf (&v)[16], float2* slot, int lane) {
+    // pass 1: radix 16 over z[j + 64q]; y[16j + r]
+    dft16<INV>(v);
+    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) lds_st(slot, 17 * lane + r, v[r]);
+    wave_lds_sync();
+    // pass 2: radix 16, span 16: inputs y[j + 64q] * W256^(qk), k = j % 16;
+    // outputs y2[(j - k) 16 + k + 16 r]
+    const int k = lane & 15, rb = pad16(lane);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = lds_ld(slot, rb + 68 * q);
+#pragma unroll
+    for (int q = 1; q < 16; ++q) v[q] = cmul(v[q], twiddle<INV>(8 * q * k));
+    dft16<INV>(v);
+    wave_lds_sync();
+    const int wb = 272 * (lane >> 4) + k;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) lds_st(slot, wb + 17 * r, v[r]);
+    wave_lds_sync();
+    // pass 3: radix 4, span 256: butterflies jj = l + 64s over y2[jj + 256q] * W1024^(q jj)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) v[a] = lds_ld(slot, rb + 68 * a);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int jj = lane + 64 * s;
+        v[s + 4] = cmul(v[s + 4], twiddle<INV>(2 * jj));
+        v[s + 8] = cmul(v[s + 8], twiddle<INV>(4 * jj));
+        v[s + 12] = cmul(v[s + 12], twiddle<INV>(6 * jj));
+        dft4<INV>(v[s], v[s + 4], v[s + 8], v[s + 12]);
+    }
+}
+
+// ---- STFT -------------------------------------------------------------------------------
+struct StftArgs {
+    const float* x;    // [B, L]
+    const float* w;    // [2048]
+    float2* out;       // [B, 1025, T] complex
+    int64_t L;
+    int64_t frames;    // B * T
+    int T;
+    int hop;
+    int offset;        // 1024 when centred (reflect padding), else 0
+    float norm;
+};
+
+template <int TF>
+__global__ __launch_bounds__(kThreads) void stft_kernel(StftArgs a) {
+    __shared__ __attribute__((aligned(16))) float2 lds[TF * kSlot];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t g0 = (int64_t)blockIdx.x * TF;
+    for (int tl = wave; tl < TF; tl += kWaves) {
+        const int64_t g = g0 + tl;
+        if (g >= a.frames) break;
+        float2* slot = lds + tl * kSlot;
+        const int64_t b = g / a.T;
+        const int t = (int)(g - b * a.T);
+        const float* xb = a.x + b * a.L;
+        const int64_t start = (int64_t)t * a.hop - a.offset;
+        cf v[16];
+        if (start >= 0 && start + kN <= a.L) {
+            const float* xs = xb + start;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int n = 2 * (lane + 64 * q);
+                v[q] = cf{xs[n] * a.w[n], xs[n + 1] * a.w[n + 1]};
+            }
+        } else {
+            // reflect once about the ends, then clamp (the reference's pad_reflect rule)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int n = 2 * (lane + 64 * q);
+                float e[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    int64_t c = start + n + h;
+                    if (c < 0) c = -c;
+                    if (c >= a.L) c = 2 * (a.L - 1) - c;
+                    c = c < 0 ? 0 : (c > a.L - 1 ? a.L - 1 : c);
+                    e[h] = xb[c] * a.w[n + h];
+                }
+                v[q] = cf{e[0], e[1]};
+            }
+        }
+        fft1024<false>(v, slot, lane);
+        wave_lds_sync();
+#pragma unroll
+        for (int q = 0; q < 16; ++q) lds_st(slot, pad16(lane) + 68 * q, v[q]);
+        wave_lds_sync();
+        // real split, in place: lane l turns the pair (Z[f], Z[1024 - f]), f = 1 + l + 64a,
+        // into (X[f], X[1024 - f]); lane 0 also writes X[0] and X[1024] from Z[0].
+        cf z0{0.f, 0.f};
+        if (lane == 0) z0 = lds_ld(slot, 0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int f = 1 + lane + 64 * q, gg = kN / 2 - f;
+            const cf zf = lds_ld(slot, pad16(f)), zg = lds_ld(slot, pad16(gg));
+            const cf A{zf.x + zg.x, zf.y - zg.y}, Bv{zf.x - zg.x, zf.y + zg.y};
+            const cf P = cmul(twiddle<false>(f), Bv);
+            lds_st(slot, pad16(f), cf{0.5f * (A.x + P.y), 0.5f * (A.y - P.x)});
+            lds_st(slot, pad16(gg), cf{0.5f * (A.x - P.y), -0.5f * (A.y + P.x)});
+        }
+        if (lane == 0) {
+            lds_st(slot, 0, cf{z0.x + z0.y, 0.f});
+            lds_st(slot, pad16(kN / 2), cf{z0.x - z0.y, 0.f});
+        }
+    }
+    __syncthreads();
+    // transposed store: thread -> (frame tl, bins fr, fr + 256/TF, ...)
+    const int tl = threadIdx.x % TF, fr = threadIdx.x / TF;
+    const int64_t g = g0 + tl;
+    if (g >= a.frames) return;
+    const int64_t b = g / a.T;
+    const int64_t t = g - b * a.T;
+    float2* dst = a.out + b * kBins * (int64_t)a.T + t;
+    const float2* src = lds + tl * kSlot;
+    for (int f = fr; f < kBins; f += kThreads / TF) {
+        const float2 X = src[pad16(f)];
+        dst[(int64_t)f * a.T] = make_float2(X.x * a.norm, X.y * a.norm);
+    }
+}
+
+// ---- iSTFT ------------------------------------------------------------------------------
+struct IstftFramesArgs {
+    const void* spec;   // [B, 1025, T] complex, f32 or bf16
+    const float* w;
+    float* frames;      // [B*T, 2048]
+    int64_t frames_n;   // B * T
+    int T;
+    float spec_scale;
+};
+
+template <int SDT>
+__device__ __forceinline__ float2 load_bin(const void* spec, int64_t i) {
+    if constexpr (SDT == F32) {
+        return static_cast<const float2*>(spec)[i];
+    } else {
+        const uint32_t u = static_cast<const uint32_t*>(spec)[i];
+        return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+    }
+}
+
+template <int TF, int SDT>
+__global__ __launch_bounds__(kThreads) void istft_frames_kernel(IstftFramesArgs a) {
+    __shared__ __attribute__((aligned(16))) float2 lds[TF * kSlot];
+    const int64_t g0 = (int64_t)blockIdx.x * TF;
+    {
+        const int tl = threadIdx.x % TF, fr = threadIdx.x / TF;
+        const int64_t g = g0 + tl;
+        if (g < a.frames_n) {
+            const int64_t b = g / a.T;
+            const int64_t t = g - b * a.T;
+            const int64_t base = b * kBins * (int64_t)a.T + t;
+            float2* slot = lds + tl * kSlot;
+            for (int f = fr; f < kBins; f += kThreads / TF) {
+                const float2 X = load_bin<SDT>(a.spec, base + (int64_t)f * a.T);
+                slot[pad16(f)] = make_float2(X.x * a.spec_scale, X.y * a.spec_scale);
+            }
+        }
+    }
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int tl = wave; tl < TF; tl += kWaves) {
+        const int64_t g = g0 + tl;
+        if (g >= a.frames_n) break;
+        float2* slot = lds + tl * kSlot;
+        // inverse real split, in place: (X[k], X[1024 - k]) -> (Z[k], Z[1024 - k]) scaled by 2;
+        // Z[0] from the real parts of X[0] and X[1024] (their imaginary parts drop out).
+        cf x0{0.f, 0.f}, xn{0.f, 0.f};
+        if (lane == 0) {
+            x0 = lds_ld(slot, 0);
+            xn = lds_ld(slot, pad16(kN / 2));
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int k = 1 + lane + 64 * q, gg = kN / 2 - k;
+            const cf xk = lds_ld(slot, pad16(k)), xg = lds_ld(slot, pad16(gg));
+            const cf A{xk.x + xg.x, xk.y - xg.y}, Bv{xk.x - xg.x, xk.y + xg.y};
+            const cf Q = cmul(Bv, twiddle<true>(k));
+            lds_st(slot, pad16(k), cf{A.x - Q.y, A.y + Q.x});
+            lds_st(slot, pad16(gg), cf{A.x + Q.y, Q.x - A.y});
+        }
+        if (lane == 0) lds_st(slot, 0, cf{x0.x + xn.x, x0.x - xn.x});
+        wave_lds_sync();
+        cf v[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = lds_ld(slot, pad16(lane) + 68 * q);
+        fft1024<true>(v, slot, lane);
+        // lane l holds 2048 * (x[2m], x[2m + 1]), m = l + 64a
+        float2* dst = reinterpret_cast<float2*>(a.frames + g * kN);
+        constexpr float kInvN = 1.0f / (float)kN;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int m = lane + 64 * q;
+            dst[m] = make_float2(v[q].x * a.w[2 * m] * kInvN, v[q].y * a.w[2 * m + 1] * kInvN);
+        }
+    }
+}
+
+struct OlaArgs {
+    const float* frames;  // [B*T, 2048]
+    const float* w;
+    float* out;           // [B, out_len]
+    int64_t total;        // B * out_len
+    int64_t out_len;
+    int64_t valid;        // samples of the (trimmed) signal; out_len - valid zeros follow
+    int T;
+    int hop;
+    int offset;           // 1024 when centred
+};
+
+__global__ __launch_bounds__(256) void istft_ola_kernel(OlaArgs a) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.total; i += (int64_t)gridDim.x * 256) {
+        const int64_t b = i / a.out_len;
+        const int64_t s = i - b * a.out_len;
+        float y = 0.0f;
+        if (s < a.valid) {
+            const int64_t sf = s + a.offset;
+            const int64_t thi = min((int64_t)a.T - 1, sf / a.hop);
+            const int64_t tlo = sf >= kN ? (sf - kN) / a.hop + 1 : 0;
+            float acc = 0.0f, ws = 0.0f;
+            const float* fb = a.frames + b * (int64_t)a.T * kN;
+            for (int64_t t = tlo; t <= thi; ++t) {
+                const int n = (int)(sf - t * a.hop);
+                acc += fb[t * kN + n];
+                const float wn = a.w[n];
+                ws = __fadd_rn(ws, __fmul_rn(wn, wn));
+            }
+            y = ws > 1.0e-8f ? acc / ws : acc;
+        }
+        a.out[i] = y;
+    }
+}
+
+__global__ __launch_bounds__(256) void hann_kernel(float* out, int64_t size) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= size) return;
+    const float phase = (float)i * (6.28318530717958647692f / (float)size);
+    out[i] = 0.5f * (1.0f - cosf(phase));
+}
+
+int check_fixed_size(const char* op, int64_t n_fft, int64_t win_length, int64_t window_numel) {
+    MBRT_REQUIRE(n_fft == kN && win_length == kN && window_numel == kN, MBRT_E_SHAPE,
+                 "%s: only n_fft=2048, win_length=2048 with a 2048-sample window is supported "
+                 "(got n_fft=%lld, win_length=%lld, window %lld)", op, (long long)n_fft,
+                 (long long)win_length, (long long)window_numel);
+    return MBRT_OK;
+}
+
+int64_t grid_for(int64_t work, int64_t per_block) {
+    return std::min<int64_t>(ceil_div(work, per_block), int64_t(1) << 20);
+}
+
+}  // namespace
+}  // namespace mbrt
+
+using namespace mbrt;
+
+extern "C" {
+
+int64_t mbrt_stft_num_frames(int64_t length, int64_t hop, int center) {
+    if (length < 0 || hop < 1) return -1;
+    const int64_t padded = length + (center ? kN : 0);
+    if (padded < kN) return 0;
+    return (padded - kN) / hop + 1;
+}
+
+int mbrt_hann_window(float* out, int64_t size, mbrt_stream_t stream) {
+    const char* op = "mbrt_hann_window";
+    MBRT_REQUIRE(size >= 0 && size < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: bad size %lld", op, (long long)size);
+    if (size == 0) return MBRT_OK;
+    MBRT_REQUIRE(out != nullptr, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
+    if (size == 1) return mbrt_fill(out, F32, 1, 1.0, stream);
+    hipLaunchKernelGGL(hann_kernel, dim3((unsigned)ceil_div(size, 256)), dim3(256), 0, as_stream(stream), out, size);
+    return check_launch(op);
+}
+
+int mbrt_stft(const float* signal, const float* window, float* out, int64_t batch, int64_t length, int64_t n_fft,
+              int64_t hop, int64_t win_length, int64_t window_numel, int center, int normalized,
+              mbrt_stream_t stream) {
+    const char* op = "mbrt_stft";
+    int s = check_fixed_size(op, n_fft, win_length, window_numel);
+    if (s != MBRT_OK) return s;
+    MBRT_REQUIRE(batch >= 0 && length >= 1 && hop >= 1 && hop < (1 << 30), MBRT_E_SHAPE,
+                 "%s: bad shape (batch %lld, length %lld, hop %lld)", op, (long long)batch, (long long)length,
+                 (long long)hop);
+    const int64_t T = mbrt_stft_num_frames(length, hop, center);
+    MBRT_REQUIRE(T >= 1, MBRT_E_SHAPE, "%s: signal of %lld samples is shorter than n_fft=2048", op,
+                 (long long)length);
+    MBRT_REQUIRE(T < (1 << 30), MBRT_E_SHAPE, "%s: too many frames", op);
+    if (batch == 0) return MBRT_OK;
+    MBRT_REQUIRE(signal && window && out, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
+    MBRT_REQUIRE(aligned(out, 8), MBRT_E_ALIGN, "%s: out must be 8-byte aligned", op);
+    StftArgs a{};
+    a.x = signal;
+    a.w = window;
+    a.out = reinterpret_cast<float2*>(out);
+    a.L = length;
+    a.frames = batch * T;
+    a.T = (int)T;
+    a.hop = (int)hop;
+    a.offset = center ? kN / 2 : 0;
+    a.norm = normalized ? 1.0f / std::sqrt((float)kN) : 1.0f;
+    const int64_t blocks = ceil_div(a.frames, kTF);
+    MBRT_REQUIRE(blocks < kMaxGridX, MBRT_E_SHAPE, "%s: too many frames", op);
+    hipLaunchKernelGGL((stft_kernel<kTF>), dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream), a);
+    return check_launch(op);
+}
+
+int64_t mbrt_istft_output_length(int64_t frames, int64_t hop, int center, int64_t length) {
+    if (frames < 1 || hop < 1) return -1;
+    if (length > 0) return length;
+    const int64_t full = kN + (frames - 1) * hop;
+    return center ? full - kN : full;
+}
+
+int64_t mbrt_istft_workspace_bytes(int64_t batch, int64_t frames) {
+    if (batch < 0 || frames < 0) return -1;
+    return batch * frames * kN * (int64_t)sizeof(float);
+}
+
+int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out, int64_t batch,
+               int64_t freq_bins, int64_t frames, int64_t n_fft, int64_t hop, int64_t win_length,
+               int64_t window_numel, int center, int normalized, int64_t length, void* workspace,
+               int64_t workspace_bytes, mbrt_stream_t stream) {
+    const char* op = "mbrt_istft";
+    int s = check_fixed_size(op, n_fft, win_length, window_numel);
+    if (s != MBRT_OK) return s;
+    MBRT_REQUIRE(freq_bins == kBins, MBRT_E_SHAPE, "%s: %lld frequency bins (expected 1025)", op,
+                 (long long)freq_bins);
+    MBRT_REQUIRE(spec_dtype == F32 || spec_dtype == BF16, MBRT_E_UNSUPPORTED_DTYPE,
+                 "%s: spectrum must be F32 or BF16", op);
+    MBRT_REQUIRE(batch >= 0 && frames >= 1 && frames < (1 << 30) && hop >= 1 && hop < (1 << 30), MBRT_E_SHAPE,
+                 "%s: bad shape (batch %lld, frames %lld, hop %lld)", op, (long long)batch, (long long)frames,
+                 (long long)hop);
+    const int64_t out_len = mbrt_istft_output_length(frames, hop, center, length);
+    if (batch == 0 || out_len == 0) return MBRT_OK;
+    MBRT_REQUIRE(spec && window && out && workspace, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
+    MBRT_REQUIRE(workspace_bytes >= mbrt_istft_workspace_bytes(batch, frames), MBRT_E_INVALID_ARG,
+                 "%s: workspace of %lld bytes, %lld needed", op, (long long)workspace_bytes,
+                 (long long)mbrt_istft_workspace_bytes(batch, frames));
+    MBRT_REQUIRE(aligned(workspace, 8) && aligned(spec, spec_dtype == F32 ? 8 : 4), MBRT_E_ALIGN,
+                 "%s: spectrum and workspace must be aligned to their complex element", op);
+    hipStream_t st = as_stream(stream);
+    IstftFramesArgs fa{};
+    fa.spec = spec;
+    fa.w = window;
+    fa.frames = static_cast<float*>(workspace);
+    fa.frames_n = batch * frames;
+    fa.T = (int)frames;
+    fa.spec_scale = normalized ? std::sqrt((float)kN) : 1.0f;
+    const int64_t blocks = ceil_div(fa.frames_n, kTF);
+    MBRT_REQUIRE(blocks < kMaxGridX, MBRT_E_SHAPE, "%s: too many frames", op);
+    if (spec_dtype == F32)
+        hipLaunchKernelGGL((istft_frames_kernel<kTF, F32>), dim3((unsigned)blocks), dim3(kThreads), 0, st, fa);
+    else
+        hipLaunchKernelGGL((istft_frames_kernel<kTF, BF16>), dim3((unsigned)blocks), dim3(kThreads), 0, st, fa);
+    s = check_launch(op);
+    if (s != MBRT_OK) return s;
+    OlaArgs oa{};
+    oa.frames = fa.frames;
+    oa.w = window;
+    oa.out = out;
+    oa.out_len = out_len;
+    oa.total = batch * out_len;
+    const int64_t full = kN + (frames - 1) * hop;
+    oa.valid = std::min<int64_t>(out_len, center ? full - kN : full);
+    oa.T = (int)frames;
+    oa.hop = (int)hop;
+    oa.offset = center ? kN / 2 : 0;
+    hipLaunchKernelGGL(istft_ola_kernel, dim3((unsigned)grid_for(oa.total, 256)), dim3(256), 0, st, oa);
+    return check_launch(op);
+}
+
+}  // extern "C"

@@ -325,6 +325,60 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tens
     return out
 
 
+N_FFT = 2048
+
+
+def hann_window(size: int = N_FFT, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Periodic Hann window [size] f32 on the current device."""
+    if out is None:
+        out = torch.empty(size, dtype=torch.float32, device="cuda")
+    _contig(out)
+    _abi.call("mbrt_hann_window", _p(out), out.numel(), _s(stream))
+    return out
+
+
+def stft_num_frames(length: int, hop: int, center: bool = True) -> int:
+    return int(_abi.lib().mbrt_stft_num_frames(length, hop, int(center)))
+
+
+def stft(signal: torch.Tensor, window: torch.Tensor, hop: int, center: bool = True, normalized: bool = False,
+         out: torch.Tensor | None = None, n_fft: int = N_FFT, win_length: int = N_FFT, stream=None) -> torch.Tensor:
+    """signal [B, L] (or [L]) f32 -> complex spectrogram [B, 1025, T, 2] f32."""
+    x = signal.reshape(1, -1) if signal.dim() == 1 else signal
+    _contig(x, window)
+    B, L = x.shape
+    T = stft_num_frames(L, hop, center)
+    if out is None:
+        out = torch.empty((B, n_fft // 2 + 1, max(T, 0), 2), dtype=torch.float32, device=x.device)
+    _contig(out)
+    _abi.call("mbrt_stft", _p(x), _p(window), _p(out), B, L, n_fft, hop, win_length, window.numel(), int(center),
+              int(normalized), _s(stream))
+    return out
+
+
+def istft_output_length(frames: int, hop: int, center: bool = True, length: int = -1) -> int:
+    return int(_abi.lib().mbrt_istft_output_length(frames, hop, int(center), length))
+
+
+def istft(spec: torch.Tensor, window: torch.Tensor, hop: int, center: bool = True, normalized: bool = False,
+          length: int = -1, out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+          n_fft: int = N_FFT, win_length: int = N_FFT, stream=None) -> torch.Tensor:
+    """spec [B, 1025, T, 2] f32/bf16 -> waveform [B, istft_output_length(T, hop, center, length)] f32."""
+    _contig(spec, window)
+    B, F, T, _ = spec.shape
+    n_out = istft_output_length(T, hop, center, length)
+    if out is None:
+        out = torch.empty((B, max(n_out, 0)), dtype=torch.float32, device=spec.device)
+    _contig(out)
+    need = int(_abi.lib().mbrt_istft_workspace_bytes(B, T))
+    if workspace is None:
+        workspace = torch.empty(max(need, 0) // 4, dtype=torch.float32, device=spec.device)
+    _abi.call("mbrt_istft", _p(spec), dtype_code(spec), _p(window), _p(out), B, F, T, n_fft, hop, win_length,
+              window.numel(), int(center), int(normalized), length, _p(workspace),
+              workspace.numel() * workspace.element_size(), _s(stream))
+    return out
+
+
 # ---- host-side tables -----------------------------------------------------------------------
 
 def mel_band_layout(sample_rate: float = 44100.0, n_fft: int = 2048, n_bands: int = 60, channels: int = 2):

@@ -96,11 +96,22 @@ SIGNATURES: dict[str, list] = {
     "mbrt_band_mask_merge": [P, C.POINTER(P), I, I, P, P, I, P, I, P, I, L, L, L, L, L, P],
     "mbrt_zero_dc": [P, I, L, L, L, P],
     "mbrt_attention": [P, P, P, I, P, I, L, L, L, L, Fl, P],
+    "mbrt_hann_window": [P, L, P],
+    "mbrt_stft_num_frames": [L, L, I],
+    "mbrt_stft": [P, P, P, L, L, L, L, L, L, I, I, P],
+    "mbrt_istft_output_length": [L, L, I, L],
+    "mbrt_istft_workspace_bytes": [L, L],
+    "mbrt_istft": [P, I, P, P, L, L, L, L, L, L, L, I, I, L, P, L, P],
     "mbrt_mel_band_layout": [D, I, I, I, P, L, C.POINTER(C.c_int64), P],
     "mbrt_band_csr": [P, L, L, P, P, P, P],
     "mbrt_rotary_tables": [P, P, L, L, Fl],
 }
-_RESTYPE = {"mbrt_last_error": C.c_char_p}
+_RESTYPE = {
+    "mbrt_last_error": C.c_char_p,
+    "mbrt_stft_num_frames": C.c_int64,
+    "mbrt_istft_output_length": C.c_int64,
+    "mbrt_istft_workspace_bytes": C.c_int64,
+}
 
 
 class MbrtError(RuntimeError):

@@ -305,3 +305,159 @@ def attention(q, k, v, dt, odt, scale=0.0, mode=EXACT):
     out = empty((BH, nq, D), odt)
     lib().orc_attention(_p(q), _p(k), _p(v), dt, _p(out), odt, L(BH), L(nq), L(nk), L(D), C.c_float(scale), mode)
     return out
+
+
+# ---- STFT / iSTFT, n_fft = win_length = 2048 (src/stft_cuda_tile.cu) ----------------------
+# Restated in numpy float64: the frame DFT is evaluated with numpy's FFT (an exact-maths
+# evaluator, pinned in tests against a direct O(N^2) DFT and torch.stft / torch.istft).
+
+N_FFT = 2048
+N_BINS = N_FFT // 2 + 1
+
+
+def hann_window(size: int) -> np.ndarray:
+    """src/stft_cuda_tile.cu:503-528: w[n] = 0.5 (1 - cos(n * (2 pi / size))), formed in f32
+    (phase step and product rounded to f32 as the kernel does; cos rounded once)."""
+    if size <= 0:
+        return np.empty(0, np.float32)
+    if size == 1:
+        return np.ones(1, np.float32)
+    step = np.float32(np.float32(6.28318530717958647692) / np.float32(size))
+    phase = np.arange(size, dtype=np.float32) * step
+    c = np.cos(phase.astype(np.float64)).astype(np.float32)
+    return (np.float32(0.5) * (np.float32(1.0) - c)).astype(np.float32)
+
+
+def hann_den(size: int) -> np.ndarray:
+    """0.5 (1 + |cos|): the magnitude 1 - cos is a difference of."""
+    if size <= 1:
+        return np.ones(max(size, 0))
+    step = np.float32(np.float32(6.28318530717958647692) / np.float32(size))
+    phase = np.arange(size, dtype=np.float32) * step
+    return 0.5 * (1.0 + np.abs(np.cos(phase.astype(np.float64))))
+
+
+def stft_num_frames(length: int, hop: int, center: bool = True) -> int:
+    """src/stft_cuda_tile.cu:544-551: T = (padded - n_fft) / hop + 1."""
+    padded = length + (N_FFT if center else 0)
+    return 0 if padded < N_FFT else (padded - N_FFT) // hop + 1
+
+
+def stft_frames(x, hop: int, center: bool = True) -> np.ndarray:
+    """Frames [B, T, 2048] (float64) of the signal, reflect-padded by n_fft/2 when centred
+    (src/stft_cuda_tile.cu:544-548 with Tensor::pad_reflect's index rule,
+    src/tensor_cuda_glue.cu:462-490: reflect once about the end samples, then clamp)."""
+    x = np.asarray(x, np.float32)
+    x = x.reshape(1, -1) if x.ndim == 1 else x
+    B, Ls = x.shape
+    off = N_FFT // 2 if center else 0
+    T = stft_num_frames(Ls, hop, center)
+    if T < 1:
+        raise ValueError("signal shorter than n_fft")
+    c = np.arange(T, dtype=np.int64)[:, None] * hop + np.arange(N_FFT, dtype=np.int64)[None, :] - off
+    c = np.where(c < 0, -c, c)
+    c = np.where(c >= Ls, 2 * (Ls - 1) - c, c)
+    c = np.clip(c, 0, Ls - 1)
+    return x[:, c].astype(np.float64)
+
+
+def _stft_norm() -> float:
+    return float(np.float32(1.0) / np.sqrt(np.float32(N_FFT)))
+
+
+def stft(x, window, hop: int, center: bool = True, normalized: bool = False) -> np.ndarray:
+    """src/stft_cuda_tile.cu:530-598: out[b, f, t] = sum_n frame_t[n] w[n] exp(-2 pi i f n / 2048)
+    for f = 0..1024, as [B, 1025, T, 2] f32 (re, im), times the f32 1/sqrtf(2048) when
+    normalized.  Exact in double, rounded once to f32."""
+    fr = stft_frames(x, hop, center) * np.asarray(window, np.float64)[None, None, :]
+    X = np.fft.rfft(fr, axis=-1)
+    if normalized:
+        X = X * _stft_norm()
+    out = np.stack([X.real, X.imag], axis=-1).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(out.astype(np.float32))
+
+
+def stft_den(x, window, hop: int, center: bool = True, normalized: bool = False) -> np.ndarray:
+    """sum_n |frame_t[n] w[n]| for every output of stft(): the magnitude each bin's sum of
+    products is taken from, broadcast over bins and (re, im)."""
+    fr = stft_frames(x, hop, center) * np.asarray(window, np.float64)[None, None, :]
+    d = np.abs(fr).sum(-1) * (_stft_norm() if normalized else 1.0)  # [B, T]
+    B, T = d.shape
+    return np.broadcast_to(d[:, None, :, None], (B, N_BINS, T, 2))
+
+
+def istft_output_length(frames: int, hop: int, center: bool = True, length: int = -1) -> int:
+    """src/stft_cuda_tile.cu:623, 700-716."""
+    if length > 0:
+        return length
+    full = N_FFT + (frames - 1) * hop
+    return full - N_FFT if center else full
+
+
+def _istft_frames(spec, dt, window, normalized):
+    S = to_f32(np.asarray(spec), dt).astype(np.float64)
+    if normalized:
+        S = S * float(np.sqrt(np.float32(N_FFT)))
+    X = (S[..., 0] + 1j * S[..., 1]).transpose(0, 2, 1)  # [B, T, 1025]
+    return X
+
+
+def _window_sum_f32(window, T: int, hop: int) -> np.ndarray:
+    """src/stft_cuda_tile.cu:462-483: sum_t w[s - t hop]^2 in f32, frames in ascending order."""
+    w = np.asarray(window, np.float32)
+    ww = (w * w).astype(np.float32)
+    full = N_FFT + (T - 1) * hop
+    ws = np.zeros(full, np.float32)
+    for t in range(T):
+        sl = slice(t * hop, t * hop + N_FFT)
+        ws[sl] = (ws[sl] + ww).astype(np.float32)
+    return ws
+
+
+def _finish(y, ws, T, hop, center, length):
+    div = np.broadcast_to(ws[None, :] > np.float32(1e-8), y.shape)
+    y = np.divide(y, np.broadcast_to(ws[None, :].astype(np.float64), y.shape), out=y.copy(), where=div)
+    full = N_FFT + (T - 1) * hop
+    if center:
+        y = y[:, N_FFT // 2: full - N_FFT // 2]
+    if length > 0:
+        if length <= y.shape[1]:
+            y = y[:, :length]
+        else:
+            y = np.concatenate([y, np.zeros((y.shape[0], length - y.shape[1]))], axis=1)
+    return y
+
+
+def istft(spec, dt, window, hop: int, center: bool = True, normalized: bool = False, length: int = -1) -> np.ndarray:
+    """src/stft_cuda_tile.cu:600-717: per frame the real inverse DFT of the Hermitian
+    extension (so the imaginary parts of bins 0 and 1024 drop out) divided by 2048, times
+    the window; overlap-added at hop spacing; divided by the f32 window sum of squares where
+    that exceeds 1e-8; centre trim of n_fft/2 at each end; `length` trims or zero-fills.
+    Exact in double (except the f32 window sum, whose threshold test must match), rounded
+    once to f32.  spec [B, 1025, T, 2] in dtype dt (F32 or BF16)."""
+    X = _istft_frames(spec, dt, window, normalized)
+    B, T, _ = X.shape
+    fr = np.fft.irfft(X, n=N_FFT, axis=-1) * np.asarray(window, np.float64)[None, None, :]
+    full = N_FFT + (T - 1) * hop
+    y = np.zeros((B, full))
+    for t in range(T):
+        y[:, t * hop: t * hop + N_FFT] += fr[:, t]
+    ws = _window_sum_f32(window, T, hop)
+    return _finish(y, ws, T, hop, center, length).astype(np.float32)
+
+
+def istft_den(spec, dt, window, hop: int, center: bool = True, normalized: bool = False,
+              length: int = -1) -> np.ndarray:
+    """Per output sample sum_t w[n_t] (|X_t[0]| + 2 sum_k |X_t[k]| + |X_t[1024]|) / 2048 (real
+    parts at bins 0 and 1024), normalised and trimmed like istft(): the magnitude of the
+    terms each sample is a sum of."""
+    X = _istft_frames(spec, dt, window, normalized)
+    B, T, _ = X.shape
+    M = (np.abs(X[..., 0].real) + 2 * np.abs(X[..., 1:-1]).sum(-1) + np.abs(X[..., -1].real)) / N_FFT  # [B, T]
+    w = np.abs(np.asarray(window, np.float64))
+    full = N_FFT + (T - 1) * hop
+    d = np.zeros((B, full))
+    for t in range(T):
+        d[:, t * hop: t * hop + N_FFT] += M[:, t:t + 1] * w[None, :]
+    ws = _window_sum_f32(window, T, hop)
+    return _finish(d, ws, T, hop, center, length)

@@ -19,6 +19,7 @@
 
 #include "hip_context.h"
 #include "mbr_tile.h"
+#include "stft_tile.h"
 #include "memory_pool.h"
 #include "tensor.h"
 
@@ -314,6 +315,22 @@ void ops(const std::string& path) {
     d.save("split_q", sq);
     d.save("split_k", sk);
     d.save("split_v", sv);
+    {
+        namespace S = cudasep::stft_tile;
+        const Tensor hann = S::hann_window(2048);
+        d.save("hann", hann);
+        const Tensor spec = S::stft(I["signal"], 2048, 441, 2048, hann);  // [2, 5000] -> [2, 1025, 12, 2]
+        d.save("stft", spec);
+        d.save("istft", S::istft(spec, 2048, 441, 2048, hann, 5000));
+        d.save("istft_bf16", S::istft(spec.to_bf16(), 2048, 441, 2048, hann));
+        bool threw = false;
+        try {
+            S::stft(I["signal"], 1024, 441, 1024, hann);
+        } catch (const std::runtime_error& e) {
+            threw = std::string(e.what()) == "custom STFT only supports n_fft=2048, win_length=2048";
+        }
+        if (!threw) throw std::runtime_error("stft_tile::stft accepted n_fft=1024");
+    }
     cudasep::g_quantize_bf16 = false;
     cudasep::HipContext::instance().synchronize();
 }

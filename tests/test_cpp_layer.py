@@ -54,6 +54,7 @@ API = [
     "cudasep::mbr_tile::residual_bf16_enabled(", "cudasep::mbr_tile::bias_bf16_enabled(",
     "cudasep::mbr_tile::norm_gamma_bf16_enabled(", "cudasep::mbr_tile::bands_per_freq_bf16_enabled(",
     "cudasep::mbr_tile::rotary_freqs_bf16_enabled(", "cudasep::mbr_tile::scaled_dot_product_attention(",
+    "cudasep::stft_tile::hann_window(", "cudasep::stft_tile::stft(", "cudasep::stft_tile::istft(",
     "cudasep::HipMemoryPool::allocate(",
     "cudasep::HipMemoryPool::deallocate(", "cudasep::HipMemoryPool::trim_cached_memory(",
 ]
@@ -127,6 +128,7 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
     stft = orc.randn((Bb, F, T, 2), seed=rng_seed, stream=13)
     m0 = orc.randn((Bb, T, J * 2), seed=rng_seed, stream=14, std=0.5)
     m1 = orc.randn((Bb, T, J * 2), seed=rng_seed, stream=15, std=0.5)
+    signal = orc.randn((2, 5000), seed=rng_seed, stream=16)
     cnt = mb["bands_per_freq"].astype(np.float32)
 
     man: list[str] = []
@@ -134,7 +136,7 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
                           ("h", h, F32), ("bias", bias, F32), ("g", g, BF16), ("attn", attn, BF16),
                           ("logits", logits, F32), ("gates", gates, F32), ("q", q, BF16), ("k", k, BF16),
                           ("cos", cos, F32), ("sin", sin, F32), ("qkv", qkv, BF16), ("stft", stft, F32),
-                          ("mask0", m0, F32), ("mask1", m1, F32), ("counts", cnt, F32),
+                          ("mask0", m0, F32), ("mask1", m1, F32), ("counts", cnt, F32), ("signal", signal, F32),
                           ("freq_indices", mb["freq_indices"].astype(np.int64), I64),
                           ("csr_off", mb["csr_offsets"].astype(np.int64), I64),
                           ("csr_ind", mb["csr_indices"].astype(np.int64), I64)]:
@@ -193,3 +195,17 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
         dt, y = _read(tmp_path, name)
         assert dt == BF16 and y.shape == (B, H, 64, Dh), (name, y.shape)
         assert_close(y, ref, BF16, name)
+    hann = orc.hann_window(2048)
+    assert_close(_read(tmp_path, "hann")[1], hann, F32, "stft_tile::hann_window", den=orc.hann_den(2048))
+    hw = _read(tmp_path, "hann")[1]
+    dt, spec = _read(tmp_path, "stft")
+    assert dt == F32 and spec.shape == (2, 1025, 12, 2)
+    assert_close(spec, orc.stft(signal, hw, 441), F32, "stft_tile::stft", den=orc.stft_den(signal, hw, 441))
+    dt, y = _read(tmp_path, "istft")
+    assert dt == F32 and y.shape == (2, 5000)
+    assert_close(y, orc.istft(spec, F32, hw, 441, length=5000), F32, "stft_tile::istft",
+                 den=orc.istft_den(spec, F32, hw, 441, length=5000))
+    sb = orc.from_f32(spec, BF16)
+    dt, y = _read(tmp_path, "istft_bf16")
+    assert dt == F32 and y.shape == (2, 11 * 441)
+    assert_close(y, orc.istft(sb, BF16, hw, 441), F32, "stft_tile::istft bf16", den=orc.istft_den(sb, BF16, hw, 441))

@@ -389,3 +389,122 @@ def test_attention_matches_numpy_and_closed_forms(orc):
     assert np.allclose(out, np.broadcast_to(v.mean(axis=1, keepdims=True), out.shape), atol=1e-6)
     ones = np.ones((1, 9, 64), np.float32) * 3.0
     assert np.allclose(orc.attention(q, orc.randn((1, 9, 64), seed=17), ones, F32, F32, 0.0), 3.0, atol=1e-6)
+
+
+# ---- STFT / iSTFT --------------------------------------------------------------------------
+
+def _direct_stft(x, w, hop, center, norm):
+    """O(N^2) DFT of frames cut with numpy's own reflect padding (not the oracle's rule)."""
+    xp = np.pad(x.astype(np.float64), ((0, 0), (1024, 1024)), mode="reflect") if center else x.astype(np.float64)
+    T = (xp.shape[1] - 2048) // hop + 1
+    n = np.arange(2048)
+    M = np.exp(-2j * np.pi * np.outer(np.arange(1025), n) / 2048)  # [1025, 2048]
+    fr = np.stack([xp[:, t * hop: t * hop + 2048] for t in range(T)], axis=1) * w.astype(np.float64)
+    X = fr @ M.T  # [B, T, 1025]
+    return (X * norm).transpose(0, 2, 1)
+
+
+def test_hann_window_closed_form_and_torch(orc):
+    for size in (2048, 1000, 7, 2):
+        w = orc.hann_window(size)
+        th = torch.hann_window(size, periodic=True, dtype=torch.float64).numpy()
+        # the f32 phase (step and product rounded) and the f32 difference 1 - cos move w by
+        # a few 1e-8 at most
+        assert np.all(np.abs(w - th) <= 4e-7 * orc.hann_den(size)), size
+    assert np.array_equal(orc.hann_window(1), np.ones(1, np.float32))
+    w = orc.hann_window(2048)
+    assert w[0] == 0.0 and w[1024] == 1.0 and np.abs(w[1:1024] - w[2047:1024:-1]).max() < 4e-7
+
+
+def test_stft_oracle_matches_direct_dft(orc):
+    rng = np.random.default_rng(11)
+    w = orc.hann_window(2048)
+    for (B, L, hop, center, normalized) in [(2, 3000, 441, True, False), (1, 5000, 512, False, True),
+                                             (1, 2100, 300, True, True)]:
+        x = rng.standard_normal((B, L)).astype(np.float32)
+        norm = float(np.float32(1.0) / np.sqrt(np.float32(2048))) if normalized else 1.0
+        want = _direct_stft(x, w, hop, center, norm)
+        got = orc.stft(x, w, hop, center, normalized)
+        assert got.shape == (B, 1025, want.shape[2], 2)
+        den = orc.stft_den(x, w, hop, center, normalized)
+        err = np.abs(got[..., 0] + 1j * got[..., 1] - want) / den[..., 0]
+        assert err.max() < 1e-7, (B, L, hop, center, normalized, err.max())
+
+
+def test_stft_oracle_reflect_rule(orc):
+    """The oracle's reflect-then-clamp rule equals numpy's reflect padding whenever the
+    signal is longer than the pad, and clamps for shorter ones (Tensor::pad_reflect)."""
+    x = np.arange(3000, dtype=np.float32)[None, :]
+    fr = orc.stft_frames(x, 441, True)
+    xp = np.pad(x[0].astype(np.float64), (1024, 1024), mode="reflect")
+    for t in range(fr.shape[1]):
+        assert np.array_equal(fr[0, t], xp[t * 441: t * 441 + 2048])
+    for L in (5, 700, 1024):   # pad 1024 >= length: reflect about each end once, then clamp
+        short = np.arange(L, dtype=np.float32)[None, :]
+        fr = orc.stft_frames(short, 441, True)
+        for t in range(fr.shape[1]):
+            for n in range(0, 2048, 7):
+                c = t * 441 + n - 1024
+                if c < 0:
+                    c = -c
+                if c >= L:
+                    c = 2 * (L - 1) - c
+                c = min(max(c, 0), L - 1)
+                assert fr[0, t, n] == c, (L, t, n)
+
+
+def test_stft_oracle_matches_torch(orc):
+    rng = np.random.default_rng(12)
+    w = orc.hann_window(2048)
+    x = rng.standard_normal((2, 30000)).astype(np.float32)
+    for normalized in (False, True):
+        t = torch.stft(torch.from_numpy(x).double(), 2048, 441, 2048, torch.from_numpy(w).double(), center=True,
+                       pad_mode="reflect", normalized=normalized, onesided=True, return_complex=True).numpy()
+        got = orc.stft(x, w, 441, True, normalized)
+        den = orc.stft_den(x, w, 441, True, normalized)
+        assert (np.abs(got[..., 0] + 1j * got[..., 1] - t) / den[..., 0]).max() < 1e-7
+
+
+def test_istft_oracle_matches_torch_and_round_trips(orc):
+    rng = np.random.default_rng(13)
+    w = orc.hann_window(2048)
+    x = rng.standard_normal((2, 30000)).astype(np.float32)
+    S = orc.stft(x, w, 441, True, False)
+    T = S.shape[2]
+    n = orc.istft_output_length(T, 441, True)
+    assert n == (T - 1) * 441
+    # perfect reconstruction where frames cover the signal
+    y = orc.istft(S, F32, w, 441, True, False, length=30000)
+    assert y.shape == (2, 30000)
+    assert np.abs(y[:, :n] - x[:, :n]).max() < 1e-5 and np.all(y[:, n:] == 0)
+    # an arbitrary (inconsistent) spectrum, with DC / Nyquist imaginary parts set
+    R = rng.standard_normal(S.shape).astype(np.float32)
+    for normalized, length in ((False, -1), (True, 25000)):
+        got = orc.istft(R, F32, w, 441, True, normalized, length)
+        ti = torch.istft(torch.from_numpy(R[..., 0] + 1j * R[..., 1]).to(torch.complex128), 2048, 441, 2048,
+                         torch.from_numpy(w).double(), center=True, normalized=normalized, onesided=True,
+                         length=None if length < 0 else length).numpy()
+        den = orc.istft_den(R, F32, w, 441, True, normalized, length)
+        assert got.shape == ti.shape
+        assert (np.abs(got - ti) / np.maximum(den, 1e-30)).max() < 1e-6
+
+
+def test_istft_oracle_gaps_and_bf16(orc):
+    """hop > n_fft leaves samples no frame covers: window sum 0, output 0 (no division).
+    A bf16 spectrum is read as its f32 values."""
+    rng = np.random.default_rng(14)
+    w = orc.hann_window(2048)
+    R = rng.standard_normal((1, 1025, 4, 2)).astype(np.float32)
+    y = orc.istft(R, F32, w, 3000, False, False)
+    assert y.shape == (1, 2048 + 3 * 3000)
+    assert np.all(y[0, 2048:3000] == 0) and np.all(y[0, 5048:6000] == 0)
+    # single frame, not centred: x = irfft(X) w / w^2 = irfft(X) / w where w^2 > 1e-8
+    y0 = orc.istft(R[:, :, :1], F32, w, 3000, False, False)[0]
+    ref = np.fft.irfft(R[0, :, 0, 0] + 1j * R[0, :, 0, 1], 2048)
+    ww = (w * w).astype(np.float32)
+    ok = ww > np.float32(1e-8)
+    want = np.where(ok, ref / np.where(ok, w, 1).astype(np.float64), ref * w)
+    den = orc.istft_den(R[:, :, :1], F32, w, 3000, False, False)[0]
+    assert np.all(np.abs(y0 - want) <= 1e-6 * den)
+    Rb = orc.f32_to_bf16(R)
+    assert np.array_equal(orc.istft(Rb, BF16, w, 441, True), orc.istft(orc.bf16_to_f32(Rb), F32, w, 441, True))
