@@ -170,6 +170,25 @@ def build_ops(torch, mbrt, bands):
         op.next = True
         op.run = lambda b: mbrt.attention(b["q"], b["k"], b["v"], b["y"], 0.125)
         ops.append(op)
+    # STFT / iSTFT (n_fft 2048, hop 441, Hann, centred) of the chunk: 4 x 2 channels x 352800
+    # samples <-> [8, 1025, 801, 2].  Memory-bound; reported in config.next_ops with GB/s of
+    # algorithmic bytes (signal + spectrum; the iSTFT's frame workspace is not counted).
+    win = mbrt.hann_window(2048)
+    Bs, Ls, Ts = 8, 352800, 801
+    sb = Bs * Ls * 4 + 2048 * 4 + Bs * 1025 * Ts * 2 * 4
+    op = Op("stft_chunk_f32", sb, lambda: dict(x=randn((Bs, Ls)), y=torch.empty((Bs, 1025, Ts, 2), device=dev)),
+            "stft_kernel")
+    op.next = True
+    op.run = lambda b: mbrt.stft(b["x"], win, 441, out=b["y"])
+    ops.append(op)
+    for stag, sdt, ssz in (("f32", torch.float32, 4), ("bf16", bf16, 2)):
+        op = Op(f"istft_chunk_{stag}", Bs * 1025 * Ts * 2 * ssz + 2048 * 4 + Bs * Ls * 4,
+                (lambda sdt=sdt: dict(s=randn((Bs, 1025, Ts, 2), sdt), y=torch.empty((Bs, Ls), device=dev),
+                                      w=torch.empty(Bs * Ts * 2048, device=dev))),
+                "istft_frames_kernel")
+        op.next = True
+        op.run = lambda b: mbrt.istft(b["s"], win, 441, length=Ls, out=b["y"], workspace=b["w"])
+        ops.append(op)
     return ops
 
 
@@ -338,10 +357,15 @@ def main():
     tot_ms = 0.0
     for op in [o for o in ops if o.next]:
         ms = statistics.mean(op.times_ms)
-        tf = op.flops / (ms * 1e-3) / 1e12
-        next_ops[op.name] = {"flops": op.flops, "bytes": op.bytes, "ms": round(ms, 5), "tflops": round(tf, 1),
-                             "frac_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                             "gbs": round(op.bytes / (ms * 1e-3) / 1e9, 1), "kernel": op.kernel}
+        gbs = op.bytes / (ms * 1e-3) / 1e9
+        if op.flops > 0:
+            tf = op.flops / (ms * 1e-3) / 1e12
+            next_ops[op.name] = {"flops": op.flops, "bytes": op.bytes, "ms": round(ms, 5), "tflops": round(tf, 1),
+                                 "frac_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                 "gbs": round(gbs, 1), "kernel": op.kernel}
+        else:
+            next_ops[op.name] = {"bytes": op.bytes, "ms": round(ms, 5), "gbs": round(gbs, 1),
+                                 "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "kernel": op.kernel}
     ops = [o for o in ops if not o.next]
     for op in ops:
         ms = statistics.mean(op.times_ms)

@@ -31,17 +31,29 @@ namespace {
 
 constexpr int kN = 2048;        // n_fft = win_length
 constexpr int kBins = kN / 2 + 1;
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
 #ifndef MBRT_STFT_TF
 #define MBRT_STFT_TF 8
 #endif
-constexpr int kTF = MBRT_STFT_TF;  // frames per workgroup
+// Frames per workgroup; one wave per frame.  A workgroup holds kTF frame slots and the
+// twiddle table in LDS (78 KB at kTF = 8: two workgroups, 16 waves, per CU).
+constexpr int kTF = MBRT_STFT_TF;
+#ifndef MBRT_STFT_XCD
+#define MBRT_STFT_XCD 8
+#endif
+// Frame blocks are dealt to the XCDs in runs of this many consecutive blocks, so the blocks
+// that share the cache lines of a bin row ([B, 1025, T] holds kTF frames of a bin in
+// 8 kTF bytes) meet in one L2.
+constexpr uint32_t kXcdRun = MBRT_STFT_XCD;
 // LDS slot of one frame, in complex elements: holds padded indices up to pad(1024) = 1088;
 // 1092 complex = 2184 words = 8 (mod 64) words, so the transposed pass (kTF lanes of one
 // bin reading kTF slots) spreads over all banks.
 constexpr int kSlot = 1092;
-static_assert(kTF >= 1 && kTF <= 16 && (kThreads % kTF) == 0, "frames per workgroup");
+constexpr int kTwHalf = 1024;  // LDS twiddles W^i, i < 1024 (W^(i + 1024) = -W^i)
+// W^i sits at i + i/32 in LDS: the strided index sets of the passes (8qk over k, 2q(l + 64s)
+// over l) then fall on distinct banks.
+constexpr int kTwSlots = kTwHalf + kTwHalf / 32;
+__device__ __forceinline__ int tw_pos(int i) { return i + (i >> 5); }
+static_assert(kTF == 4 || kTF == 8 || kTF == 16, "frames per workgroup");
 
 __device__ __forceinline__ int pad16(int p) { return p + (p >> 4); }
 
@@ -102,11 +114,21 @@ template <bool INV>
 __device__ __forceinline__ cf rot(cf a) {
     return INV ? cf{-a.y, a.x} : cf{a.y, -a.x};
 }
-// W^i (forward) or its conjugate (inverse), 0 <= i < 2048
+// W^i (forward) or its conjugate (inverse), 0 <= i < 2048, from the LDS half table:
+// W^(i + 1024) = -W^i flips both signs.
 template <bool INV>
-__device__ __forceinline__ cf twiddle(int i) {
-    const float2 w = reinterpret_cast<const float2*>(kTwiddles.v)[i];
-    return INV ? cf{w.x, -w.y} : cf{w.x, w.y};
+__device__ __forceinline__ cf twiddle(const float2* tw, int i) {
+    const float2 t = tw[tw_pos(i & (kTwHalf - 1))];
+    const uint32_t s = (uint32_t)(i >> 10) << 31;
+    return {__uint_as_float(__float_as_uint(t.x) ^ s),
+            __uint_as_float(__float_as_uint(t.y) ^ s ^ (INV ? 0x80000000u : 0u))};
+}
+
+// Copies W^i, i < 1024, into the workgroup's LDS table (all threads take part).
+template <int NT>
+__device__ __forceinline__ void load_twiddles(float2* tw) {
+    const float2* src = reinterpret_cast<const float2*>(kTwiddles.v);
+    for (int i = threadIdx.x; i < kTwHalf; i += NT) tw[tw_pos(i)] = src[i];
 }
 
 template <bool INV>
@@ -171,10 +193,11 @@ __device__ __forceinline__ cf lds_ld(const float2* s, int i) {
 }
 __device__ __forceinline__ void lds_st(float2* s, int i, cf v) { s[i] = make_float2(v.x, v.y); }
 
-// 1024-point FFT of one frame by one wave.  In: lane l holds z[l + 64a] in v[a].  Out: lane
-// l holds Z[l + 64a] in v[a].  The slot is scratch (previous contents are overwritten).
+// Passes 1 and 2 of the 1024-point FFT of one frame by one wave.  In: lane l holds z[l + 64a]
+// in v[a].  Out: the slot holds y2 (pass-2 output) at padded indices.  Previous slot
+// contents are overwritten.
 template <bool INV>
-__device__ __forceinline__ void fft1024(cf (&v)[16], float2* slot, int lane) {
+__device__ __forceinline__ void fft_pass12(cf (&v)[16], float2* slot, const float2* tw, int lane) {
     // pass 1: radix 16 over z[j + 64q]; y[16j + r]
     dft16<INV>(v);
     wave_lds_sync();
@@ -182,29 +205,62 @@ __device__ __forceinline__ void fft1024(cf (&v)[16], float2* slot, int lane) {
     for (int r = 0; r < 16; ++r) lds_st(slot, 17 * lane + r, v[r]);
     wave_lds_sync();
     // pass 2: radix 16, span 16: inputs y[j + 64q] * W256^(qk), k = j % 16;
-    // outputs y2[(j - k) 16 + k + 16 r]
+    // outputs y2[(j - k) 16 + k + 16 r].  W^(8qk) = W^(8 q0 k) W^(32 q1 k) for q = q0 + 4 q1:
+    // six table reads and nine products instead of fifteen reads.
     const int k = lane & 15, rb = pad16(lane);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = lds_ld(slot, rb + 68 * q);
+    const cf t1 = twiddle<INV>(tw, 8 * k), t2 = twiddle<INV>(tw, 16 * k), t3 = twiddle<INV>(tw, 24 * k);
+    const cf u1 = twiddle<INV>(tw, 32 * k), u2 = twiddle<INV>(tw, 64 * k), u3 = twiddle<INV>(tw, 96 * k);
+    const cf tq0[4] = {cf{1.f, 0.f}, t1, t2, t3}, tq1[4] = {cf{1.f, 0.f}, u1, u2, u3};
 #pragma unroll
-    for (int q = 1; q < 16; ++q) v[q] = cmul(v[q], twiddle<INV>(8 * q * k));
+    for (int q = 1; q < 16; ++q) {
+        const int q0 = q & 3, q1 = q >> 2;
+        const cf w = q0 == 0 ? tq1[q1] : (q1 == 0 ? tq0[q0] : cmul(tq0[q0], tq1[q1]));
+        v[q] = cmul(v[q], w);
+    }
     dft16<INV>(v);
     wave_lds_sync();
     const int wb = 272 * (lane >> 4) + k;
 #pragma unroll
     for (int r = 0; r < 16; ++r) lds_st(slot, wb + 17 * r, v[r]);
     wave_lds_sync();
-    // pass 3: radix 4, span 256: butterflies jj = l + 64s over y2[jj + 256q] * W1024^(q jj)
+}
+
+// Radix-4 butterfly jj of pass 3 (span 256): inputs y2[jj + 256q] * W1024^(q jj) from the slot,
+// outputs Z[jj + 256 r] in z[r].
+template <bool INV>
+__device__ __forceinline__ void pass3_butterfly(const float2* slot, const float2* tw, int jj, cf (&z)[4]) {
+    const int base = jj + (jj >> 4);  // pad16(jj + 256 q) = base + 272 q
 #pragma unroll
-    for (int a = 0; a < 16; ++a) v[a] = lds_ld(slot, rb + 68 * a);
+    for (int q = 0; q < 4; ++q) z[q] = lds_ld(slot, base + 272 * q);
+    z[1] = cmul(z[1], twiddle<INV>(tw, 2 * jj));
+    z[2] = cmul(z[2], twiddle<INV>(tw, 4 * jj));
+    z[3] = cmul(z[3], twiddle<INV>(tw, 6 * jj));
+    dft4<INV>(z[0], z[1], z[2], z[3]);
+}
+
+// 1024-point FFT of one frame by one wave.  In: lane l holds z[l + 64a] in v[a].  Out: lane
+// l holds Z[l + 64a] in v[a].
+template <bool INV>
+__device__ __forceinline__ void fft1024(cf (&v)[16], float2* slot, const float2* tw, int lane) {
+    fft_pass12<INV>(v, slot, tw, lane);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const int jj = lane + 64 * s;
-        v[s + 4] = cmul(v[s + 4], twiddle<INV>(2 * jj));
-        v[s + 8] = cmul(v[s + 8], twiddle<INV>(4 * jj));
-        v[s + 12] = cmul(v[s + 12], twiddle<INV>(6 * jj));
-        dft4<INV>(v[s], v[s + 4], v[s + 8], v[s + 12]);
+        cf z[4];
+        pass3_butterfly<INV>(slot, tw, lane + 64 * s, z);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[s + 4 * r] = z[r];
     }
+}
+
+// Real-input split of one mirror pair: from Z[f] and Z[1024 - f] (W^f = wf) writes X[f] and
+// X[1024 - f] into the slot.  f = 0 (with zg = Z[0]) yields X[0] and X[1024].
+__device__ __forceinline__ void r2c_pair(float2* slot, int f, cf zf, cf zg, cf wf) {
+    const cf A{zf.x + zg.x, zf.y - zg.y}, Bv{zf.x - zg.x, zf.y + zg.y};
+    const cf P = cmul(wf, Bv);
+    lds_st(slot, pad16(f), cf{0.5f * (A.x + P.y), 0.5f * (A.y - P.x)});
+    lds_st(slot, pad16(kN / 2 - f), cf{0.5f * (A.x - P.y), -0.5f * (A.y + P.x)});
 }
 
 // ---- STFT -------------------------------------------------------------------------------
@@ -212,87 +268,121 @@ struct StftArgs {
     const float* x;    // [B, L]
     const float* w;    // [2048]
     float2* out;       // [B, 1025, T] complex
-    int64_t L;
-    int64_t frames;    // B * T
-    int T;
+    int L;
+    uint32_t frames;   // B * T
+    FastDiv T;         // frame index -> (signal, frame in signal)
     int hop;
     int offset;        // 1024 when centred (reflect padding), else 0
+    int wvec;          // window is 8-byte aligned: read it as float2
     float norm;
 };
 
-template <int TF>
-__global__ __launch_bounds__(kThreads) void stft_kernel(StftArgs a) {
-    __shared__ __attribute__((aligned(16))) float2 lds[TF * kSlot];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t g0 = (int64_t)blockIdx.x * TF;
-    for (int tl = wave; tl < TF; tl += kWaves) {
-        const int64_t g = g0 + tl;
-        if (g >= a.frames) break;
-        float2* slot = lds + tl * kSlot;
-        const int64_t b = g / a.T;
-        const int t = (int)(g - b * a.T);
-        const float* xb = a.x + b * a.L;
-        const int64_t start = (int64_t)t * a.hop - a.offset;
-        cf v[16];
-        if (start >= 0 && start + kN <= a.L) {
-            const float* xs = xb + start;
+// Windowed frame of sample pairs: v[q] = (x[n] w[n], x[n+1] w[n+1]), n = 2 (lane + 64 q).
+__device__ __forceinline__ void load_frame(const StftArgs& a, uint32_t b, uint32_t t, int lane, cf (&v)[16]) {
+    const float* xb = a.x + (int64_t)b * a.L;
+    const int start = (int)t * a.hop - a.offset;
+    float2 w[16];
+    if (a.wvec) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) w[q] = reinterpret_cast<const float2*>(a.w)[lane + 64 * q];
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) w[q] = make_float2(a.w[2 * (lane + 64 * q)], a.w[2 * (lane + 64 * q) + 1]);
+    }
+    if (start >= 0 && start + kN <= a.L) {
+        const float* xs = xb + start;
+        if ((reinterpret_cast<uintptr_t>(xs) & 7) == 0) {
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const int n = 2 * (lane + 64 * q);
-                v[q] = cf{xs[n] * a.w[n], xs[n + 1] * a.w[n + 1]};
+                const float2 p = reinterpret_cast<const float2*>(xs)[lane + 64 * q];
+                v[q] = cf{p.x * w[q].x, p.y * w[q].y};
             }
         } else {
-            // reflect once about the ends, then clamp (the reference's pad_reflect rule)
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int n = 2 * (lane + 64 * q);
-                float e[2];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    int64_t c = start + n + h;
-                    if (c < 0) c = -c;
-                    if (c >= a.L) c = 2 * (a.L - 1) - c;
-                    c = c < 0 ? 0 : (c > a.L - 1 ? a.L - 1 : c);
-                    e[h] = xb[c] * a.w[n + h];
-                }
-                v[q] = cf{e[0], e[1]};
+                v[q] = cf{xs[n] * w[q].x, xs[n + 1] * w[q].y};
             }
         }
-        fft1024<false>(v, slot, lane);
-        wave_lds_sync();
+    } else {
+        // reflect once about the ends, then clamp (the reference's pad_reflect rule)
 #pragma unroll
-        for (int q = 0; q < 16; ++q) lds_st(slot, pad16(lane) + 68 * q, v[q]);
-        wave_lds_sync();
-        // real split, in place: lane l turns the pair (Z[f], Z[1024 - f]), f = 1 + l + 64a,
-        // into (X[f], X[1024 - f]); lane 0 also writes X[0] and X[1024] from Z[0].
-        cf z0{0.f, 0.f};
-        if (lane == 0) z0 = lds_ld(slot, 0);
+        for (int q = 0; q < 16; ++q) {
+            const int n = 2 * (lane + 64 * q);
+            float e[2];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int f = 1 + lane + 64 * q, gg = kN / 2 - f;
-            const cf zf = lds_ld(slot, pad16(f)), zg = lds_ld(slot, pad16(gg));
-            const cf A{zf.x + zg.x, zf.y - zg.y}, Bv{zf.x - zg.x, zf.y + zg.y};
-            const cf P = cmul(twiddle<false>(f), Bv);
-            lds_st(slot, pad16(f), cf{0.5f * (A.x + P.y), 0.5f * (A.y - P.x)});
-            lds_st(slot, pad16(gg), cf{0.5f * (A.x - P.y), -0.5f * (A.y + P.x)});
+            for (int h = 0; h < 2; ++h) {
+                int c = start + n + h;
+                if (c < 0) c = -c;
+                if (c >= a.L) c = 2 * (a.L - 1) - c;
+                c = c < 0 ? 0 : (c > a.L - 1 ? a.L - 1 : c);
+                e[h] = xb[c];
+            }
+            v[q] = cf{e[0] * w[q].x, e[1] * w[q].y};
+        }
+    }
+}
+
+template <int TF>
+__global__ __launch_bounds__(64 * TF) void stft_kernel(StftArgs a) {
+    constexpr int NT = 64 * TF;
+    __shared__ __attribute__((aligned(16))) float2 lds[TF * kSlot + kTwSlots];
+    float2* tw = lds + TF * kSlot;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const uint32_t g0 = xcd_runs<kXcdRun>(blockIdx.x, gridDim.x) * TF;
+    const uint32_t g = g0 + wave;  // this wave's frame
+    const bool live = g < a.frames;
+    cf v[16];
+    if (live) {
+        uint32_t b, t;
+        fdivmod(g, a.T, b, t);
+        load_frame(a, b, t, lane, v);
+    }
+    load_twiddles<NT>(tw);
+    __syncthreads();
+    if (live) {
+        float2* slot = lds + wave * kSlot;
+        fft_pass12<false>(v, slot, tw, lane);
+        // pass 3 over butterflies chosen in mirror pairs (jj, 256 - jj), so that every lane
+        // holds both Z[f] and Z[1024 - f] of its outputs: lanes 1..63 take l, 256 - l,
+        // 128 + l, 128 - l; lane 0 takes 0, 128 (each its own mirror), 64, 192.
+        const int jA = lane, jB = lane ? 256 - lane : 128;
+        const int jC = lane ? 128 + lane : 64, jD = lane ? 128 - lane : 192;
+        cf zA[4], zB[4], zC[4], zD[4];
+        pass3_butterfly<false>(slot, tw, jA, zA);
+        pass3_butterfly<false>(slot, tw, jB, zB);
+        pass3_butterfly<false>(slot, tw, jC, zC);
+        pass3_butterfly<false>(slot, tw, jD, zD);
+        wave_lds_sync();
+        // real split: Z[1024 - (jA + 256 r)] is zB[3 - r] (lane 0: zA[(4 - r) % 4]); Z[1024 -
+        // (jC + 256 r)] is zD[3 - r]; lane 0 also splits butterfly 128 against itself.
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const cf za = lane ? zB[3 - r] : zA[(4 - r) & 3];
+            r2c_pair(slot, jA + 256 * r, zA[r], za, twiddle<false>(tw, jA + 256 * r));
+            r2c_pair(slot, jC + 256 * r, zC[r], zD[3 - r], twiddle<false>(tw, jC + 256 * r));
         }
         if (lane == 0) {
-            lds_st(slot, 0, cf{z0.x + z0.y, 0.f});
-            lds_st(slot, pad16(kN / 2), cf{z0.x - z0.y, 0.f});
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+                r2c_pair(slot, 128 + 256 * r, zB[r], zB[3 - r], twiddle<false>(tw, 128 + 256 * r));
         }
     }
     __syncthreads();
-    // transposed store: thread -> (frame tl, bins fr, fr + 256/TF, ...)
+    // transposed store: thread -> (frame tl, bins fr, fr + 64, ...)
     const int tl = threadIdx.x % TF, fr = threadIdx.x / TF;
-    const int64_t g = g0 + tl;
-    if (g >= a.frames) return;
-    const int64_t b = g / a.T;
-    const int64_t t = g - b * a.T;
-    float2* dst = a.out + b * kBins * (int64_t)a.T + t;
+    const uint32_t gs = g0 + tl;
+    if (gs >= a.frames) return;
+    uint32_t bs, ts;
+    fdivmod(gs, a.T, bs, ts);
+    float2* dst = a.out + ((int64_t)bs * kBins * a.T.d + ts);
     const float2* src = lds + tl * kSlot;
-    for (int f = fr; f < kBins; f += kThreads / TF) {
+    const int64_t step = (int64_t)(NT / TF) * a.T.d;
+    dst += (int64_t)fr * a.T.d;
+#pragma unroll 4
+    for (int f = fr; f < kBins; f += NT / TF, dst += step) {
         const float2 X = src[pad16(f)];
-        dst[(int64_t)f * a.T] = make_float2(X.x * a.norm, X.y * a.norm);
+        *dst = make_float2(X.x * a.norm, X.y * a.norm);
     }
 }
 
@@ -301,8 +391,9 @@ struct IstftFramesArgs {
     const void* spec;   // [B, 1025, T] complex, f32 or bf16
     const float* w;
     float* frames;      // [B*T, 2048]
-    int64_t frames_n;   // B * T
-    int T;
+    uint32_t frames_n;  // B * T
+    FastDiv T;
+    int wvec;           // window is 8-byte aligned
     float spec_scale;
 };
 
@@ -317,59 +408,66 @@ __device__ __forceinline__ float2 load_bin(const void* spec, int64_t i) {
 }
 
 template <int TF, int SDT>
-__global__ __launch_bounds__(kThreads) void istft_frames_kernel(IstftFramesArgs a) {
-    __shared__ __attribute__((aligned(16))) float2 lds[TF * kSlot];
-    const int64_t g0 = (int64_t)blockIdx.x * TF;
+__global__ __launch_bounds__(64 * TF) void istft_frames_kernel(IstftFramesArgs a) {
+    constexpr int NT = 64 * TF;
+    __shared__ __attribute__((aligned(16))) float2 lds[TF * kSlot + kTwSlots];
+    float2* tw = lds + TF * kSlot;
+    const uint32_t g0 = xcd_runs<kXcdRun>(blockIdx.x, gridDim.x) * TF;
     {
+        // transposed spectrum load: thread -> (frame tl, bins fr, fr + 64, ...)
         const int tl = threadIdx.x % TF, fr = threadIdx.x / TF;
-        const int64_t g = g0 + tl;
+        const uint32_t g = g0 + tl;
         if (g < a.frames_n) {
-            const int64_t b = g / a.T;
-            const int64_t t = g - b * a.T;
-            const int64_t base = b * kBins * (int64_t)a.T + t;
+            uint32_t b, t;
+            fdivmod(g, a.T, b, t);
+            int64_t idx = (int64_t)b * kBins * a.T.d + t + (int64_t)fr * a.T.d;
+            const int64_t step = (int64_t)(NT / TF) * a.T.d;
             float2* slot = lds + tl * kSlot;
-            for (int f = fr; f < kBins; f += kThreads / TF) {
-                const float2 X = load_bin<SDT>(a.spec, base + (int64_t)f * a.T);
+#pragma unroll 4
+            for (int f = fr; f < kBins; f += NT / TF, idx += step) {
+                const float2 X = load_bin<SDT>(a.spec, idx);
                 slot[pad16(f)] = make_float2(X.x * a.spec_scale, X.y * a.spec_scale);
             }
         }
     }
+    load_twiddles<NT>(tw);
     __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int tl = wave; tl < TF; tl += kWaves) {
-        const int64_t g = g0 + tl;
-        if (g >= a.frames_n) break;
-        float2* slot = lds + tl * kSlot;
-        // inverse real split, in place: (X[k], X[1024 - k]) -> (Z[k], Z[1024 - k]) scaled by 2;
-        // Z[0] from the real parts of X[0] and X[1024] (their imaginary parts drop out).
-        cf x0{0.f, 0.f}, xn{0.f, 0.f};
-        if (lane == 0) {
-            x0 = lds_ld(slot, 0);
-            xn = lds_ld(slot, pad16(kN / 2));
-        }
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const uint32_t g = g0 + wave;
+    if (g >= a.frames_n) return;
+    float2* slot = lds + wave * kSlot;
+    // inverse real split, in place: (X[k], X[1024 - k]) -> (Z[k], Z[1024 - k]) scaled by 2;
+    // Z[0] from the real parts of X[0] and X[1024] (their imaginary parts drop out).
+    cf x0{0.f, 0.f}, xn{0.f, 0.f};
+    if (lane == 0) {
+        x0 = lds_ld(slot, 0);
+        xn = lds_ld(slot, pad16(kN / 2));
+    }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int k = 1 + lane + 64 * q, gg = kN / 2 - k;
-            const cf xk = lds_ld(slot, pad16(k)), xg = lds_ld(slot, pad16(gg));
-            const cf A{xk.x + xg.x, xk.y - xg.y}, Bv{xk.x - xg.x, xk.y + xg.y};
-            const cf Q = cmul(Bv, twiddle<true>(k));
-            lds_st(slot, pad16(k), cf{A.x - Q.y, A.y + Q.x});
-            lds_st(slot, pad16(gg), cf{A.x + Q.y, Q.x - A.y});
-        }
-        if (lane == 0) lds_st(slot, 0, cf{x0.x + xn.x, x0.x - xn.x});
-        wave_lds_sync();
-        cf v[16];
+    for (int q = 0; q < 8; ++q) {
+        const int k = 1 + lane + 64 * q, gg = kN / 2 - k;
+        const cf xk = lds_ld(slot, pad16(k)), xg = lds_ld(slot, pad16(gg));
+        const cf A{xk.x + xg.x, xk.y - xg.y}, Bv{xk.x - xg.x, xk.y + xg.y};
+        const cf Q = cmul(Bv, twiddle<true>(tw, k));
+        lds_st(slot, pad16(k), cf{A.x - Q.y, A.y + Q.x});
+        lds_st(slot, pad16(gg), cf{A.x + Q.y, Q.x - A.y});
+    }
+    if (lane == 0) lds_st(slot, 0, cf{x0.x + xn.x, x0.x - xn.x});
+    wave_lds_sync();
+    cf v[16];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) v[q] = lds_ld(slot, pad16(lane) + 68 * q);
-        fft1024<true>(v, slot, lane);
-        // lane l holds 2048 * (x[2m], x[2m + 1]), m = l + 64a
-        float2* dst = reinterpret_cast<float2*>(a.frames + g * kN);
-        constexpr float kInvN = 1.0f / (float)kN;
+    for (int q = 0; q < 16; ++q) v[q] = lds_ld(slot, pad16(lane) + 68 * q);
+    fft1024<true>(v, slot, tw, lane);
+    // lane l holds 2048 * (x[2m], x[2m + 1]), m = l + 64a
+    float2* dst = reinterpret_cast<float2*>(a.frames + (int64_t)g * kN);
+    constexpr float kInvN = 1.0f / (float)kN;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int m = lane + 64 * q;
-            dst[m] = make_float2(v[q].x * a.w[2 * m] * kInvN, v[q].y * a.w[2 * m + 1] * kInvN);
-        }
+    for (int q = 0; q < 16; ++q) {
+        const int m = lane + 64 * q;
+        float2 w;
+        if (a.wvec) w = reinterpret_cast<const float2*>(a.w)[m];
+        else w = make_float2(a.w[2 * m], a.w[2 * m + 1]);
+        dst[m] = make_float2(v[q].x * w.x * kInvN, v[q].y * w.y * kInvN);
     }
 }
 
@@ -377,28 +475,29 @@ struct OlaArgs {
     const float* frames;  // [B*T, 2048]
     const float* w;
     float* out;           // [B, out_len]
-    int64_t total;        // B * out_len
-    int64_t out_len;
-    int64_t valid;        // samples of the (trimmed) signal; out_len - valid zeros follow
-    int T;
-    int hop;
-    int offset;           // 1024 when centred
+    uint32_t total;       // B * out_len
+    FastDiv out_len;
+    FastDiv hop;
+    uint32_t valid;       // samples of the (trimmed) signal; out_len - valid zeros follow
+    uint32_t T;
+    uint32_t offset;      // 1024 when centred
 };
 
 __global__ __launch_bounds__(256) void istft_ola_kernel(OlaArgs a) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.total; i += (int64_t)gridDim.x * 256) {
-        const int64_t b = i / a.out_len;
-        const int64_t s = i - b * a.out_len;
+    const uint32_t hop = a.hop.d;
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < a.total; i += gridDim.x * 256) {
+        uint32_t b, s;
+        fdivmod(i, a.out_len, b, s);
         float y = 0.0f;
         if (s < a.valid) {
-            const int64_t sf = s + a.offset;
-            const int64_t thi = min((int64_t)a.T - 1, sf / a.hop);
-            const int64_t tlo = sf >= kN ? (sf - kN) / a.hop + 1 : 0;
+            const uint32_t sf = s + a.offset;
+            const uint32_t thi = min(a.T - 1, fdiv(sf, a.hop));
+            const uint32_t tlo = sf >= (uint32_t)kN ? fdiv(sf - kN, a.hop) + 1 : 0;
             float acc = 0.0f, ws = 0.0f;
-            const float* fb = a.frames + b * (int64_t)a.T * kN;
-            for (int64_t t = tlo; t <= thi; ++t) {
-                const int n = (int)(sf - t * a.hop);
-                acc += fb[t * kN + n];
+            const float* fb = a.frames + (int64_t)b * a.T * kN;
+            uint32_t n = sf - tlo * hop;
+            for (uint32_t t = tlo; t <= thi; ++t, n -= hop) {
+                acc += fb[(int64_t)t * kN + n];
                 const float wn = a.w[n];
                 ws = __fadd_rn(ws, __fmul_rn(wn, wn));
             }
@@ -463,7 +562,8 @@ int mbrt_stft(const float* signal, const float* window, float* out, int64_t batc
     const int64_t T = mbrt_stft_num_frames(length, hop, center);
     MBRT_REQUIRE(T >= 1, MBRT_E_SHAPE, "%s: signal of %lld samples is shorter than n_fft=2048", op,
                  (long long)length);
-    MBRT_REQUIRE(T < (1 << 30), MBRT_E_SHAPE, "%s: too many frames", op);
+    MBRT_REQUIRE(length <= (1 << 30) && batch * T < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many samples or frames",
+                 op);
     if (batch == 0) return MBRT_OK;
     MBRT_REQUIRE(signal && window && out, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
     MBRT_REQUIRE(aligned(out, 8), MBRT_E_ALIGN, "%s: out must be 8-byte aligned", op);
@@ -471,15 +571,16 @@ int mbrt_stft(const float* signal, const float* window, float* out, int64_t batc
     a.x = signal;
     a.w = window;
     a.out = reinterpret_cast<float2*>(out);
-    a.L = length;
-    a.frames = batch * T;
-    a.T = (int)T;
+    a.L = (int)length;
+    a.frames = (uint32_t)(batch * T);
+    a.T = make_fastdiv((uint32_t)T);
     a.hop = (int)hop;
     a.offset = center ? kN / 2 : 0;
     a.norm = normalized ? 1.0f / std::sqrt((float)kN) : 1.0f;
+    a.wvec = aligned(window, 8) ? 1 : 0;
     const int64_t blocks = ceil_div(a.frames, kTF);
     MBRT_REQUIRE(blocks < kMaxGridX, MBRT_E_SHAPE, "%s: too many frames", op);
-    hipLaunchKernelGGL((stft_kernel<kTF>), dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream), a);
+    hipLaunchKernelGGL((stft_kernel<kTF>), dim3((unsigned)blocks), dim3(64 * kTF), 0, as_stream(stream), a);
     return check_launch(op);
 }
 
@@ -522,27 +623,31 @@ int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out
     fa.spec = spec;
     fa.w = window;
     fa.frames = static_cast<float*>(workspace);
-    fa.frames_n = batch * frames;
-    fa.T = (int)frames;
+    MBRT_REQUIRE(batch * frames < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many frames", op);
+    fa.frames_n = (uint32_t)(batch * frames);
+    fa.T = make_fastdiv((uint32_t)frames);
     fa.spec_scale = normalized ? std::sqrt((float)kN) : 1.0f;
+    fa.wvec = aligned(window, 8) ? 1 : 0;
     const int64_t blocks = ceil_div(fa.frames_n, kTF);
     MBRT_REQUIRE(blocks < kMaxGridX, MBRT_E_SHAPE, "%s: too many frames", op);
     if (spec_dtype == F32)
-        hipLaunchKernelGGL((istft_frames_kernel<kTF, F32>), dim3((unsigned)blocks), dim3(kThreads), 0, st, fa);
+        hipLaunchKernelGGL((istft_frames_kernel<kTF, F32>), dim3((unsigned)blocks), dim3(64 * kTF), 0, st, fa);
     else
-        hipLaunchKernelGGL((istft_frames_kernel<kTF, BF16>), dim3((unsigned)blocks), dim3(kThreads), 0, st, fa);
+        hipLaunchKernelGGL((istft_frames_kernel<kTF, BF16>), dim3((unsigned)blocks), dim3(64 * kTF), 0, st, fa);
     s = check_launch(op);
     if (s != MBRT_OK) return s;
+    MBRT_REQUIRE(batch * out_len < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: output of %lld samples is too large", op,
+                 (long long)(batch * out_len));
     OlaArgs oa{};
     oa.frames = fa.frames;
     oa.w = window;
     oa.out = out;
-    oa.out_len = out_len;
-    oa.total = batch * out_len;
+    oa.out_len = make_fastdiv((uint32_t)out_len);
+    oa.total = (uint32_t)(batch * out_len);
     const int64_t full = kN + (frames - 1) * hop;
-    oa.valid = std::min<int64_t>(out_len, center ? full - kN : full);
-    oa.T = (int)frames;
-    oa.hop = (int)hop;
+    oa.valid = (uint32_t)std::min<int64_t>(out_len, center ? full - kN : full);
+    oa.T = (uint32_t)frames;
+    oa.hop = make_fastdiv((uint32_t)hop);
     oa.offset = center ? kN / 2 : 0;
     hipLaunchKernelGGL(istft_ola_kernel, dim3((unsigned)grid_for(oa.total, 256)), dim3(256), 0, st, oa);
     return check_launch(op);
