@@ -8,11 +8,13 @@
 // One wave transforms one frame; lane l holds z[l + 64a], a = 0..15, in registers.  The
 // 1024-point FFT runs as three Stockham passes, radix 16 (in registers), 16 and 4, with
 // two exchanges through the frame's LDS slot (index p stored at p + p/16, which keeps
-// both the strided and the contiguous access patterns free of bank conflicts).
+// both the strided and the contiguous access patterns free of bank conflicts).  The STFT
+// takes the last pass's butterflies in mirror pairs so the real split needs no exchange.
 //
-// Workgroup = 4 waves, kTF consecutive frames (flattened over batch x time).  The frames'
-// spectra stay in LDS so that the [B, F, T] layout is written (STFT) or read (iSTFT) as
-// runs of kTF consecutive frames per bin, instead of one 8-byte element per 8*T bytes.
+// Workgroup = kTF waves = kTF consecutive frames (flattened over batch x time).  The
+// frames' spectra stay in LDS so that the [B, F, T] layout is written (STFT) or read
+// (iSTFT) as runs of kTF consecutive frames per bin, instead of one 8-byte element per
+// 8*T bytes.
 //
 // STFT   one kernel: reflect-padded frame load with the window applied, FFT, real split,
 //        optional 1/sqrt(2048), transposed store.
