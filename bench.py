@@ -189,6 +189,21 @@ def build_ops(torch, mbrt, bands):
         op.next = True
         op.run = lambda b: mbrt.istft(b["s"], win, 441, length=Ls, out=b["y"], workspace=b["w"])
         ops.append(op)
+    # Chunk overlap-add: one 8 s chunk of 8 channels (4 stems x stereo) added at its offset into
+    # a 24 s output with its fade window, and the final divide by the weight sum.
+    Cc, Nc, Lc, off_c = 8, 352800, 1058400, 264600
+    fade = torch.from_numpy(mbrt.chunk_fade_window(Nc, Nc // 10)).to(dev)
+    op = Op("chunk_accumulate_8ch", Cc * Nc * 4 + Nc * 4 + 2 * Cc * Nc * 4 + 2 * Nc * 4,
+            lambda: dict(s=randn((Cc, Nc)), d=randn((Cc, Lc)), w=torch.rand(Lc, device=dev) + 1.0),
+            "accumulate_vec_kernel")
+    op.next = True
+    op.run = lambda b: mbrt.chunk_accumulate(b["d"], b["w"], b["s"], fade, off_c)
+    ops.append(op)
+    op = Op("chunk_normalize_8ch", 2 * Cc * Lc * 4 + Lc * 4,
+            lambda: dict(d=randn((Cc, Lc)), w=torch.rand(Lc, device=dev) + 1.0), "normalize_vec_kernel")
+    op.next = True
+    op.run = lambda b: mbrt.chunk_normalize(b["d"], b["w"])
+    ops.append(op)
     return ops
 
 

@@ -370,6 +370,30 @@ MBRT_API int mbrt_istft(const void* spec, int spec_dtype, const float* window, f
                         int64_t window_numel, int center, int normalized, int64_t length, void* workspace,
                         int64_t workspace_bytes, mbrt_stream_t stream);
 
+/* ---- chunk overlap-add --------------------------------------------------------- */
+
+/* dest[c, offset + i] += src[c, i] * window[i] for c < channels, i < chunk_len, and
+ * weight_sum[offset + i] += window[i]; dest is [channels, dest_len], src [channels,
+ * chunk_len], all f32.  The product and the sum are rounded separately and each element is
+ * written once per call, so calls on one stream accumulate in call order (the reference adds
+ * with atomics).  Requires 0 <= offset and offset + chunk_len <= dest_len.  Replaces
+ * chunk_tile::accumulate_chunk (src/chunk_cuda_tile.cu:18-42, 61-73). */
+MBRT_API int mbrt_chunk_accumulate(float* dest, float* weight_sum, const float* src, const float* window,
+                                   int64_t channels, int64_t chunk_len, int64_t dest_len, int64_t offset,
+                                   mbrt_stream_t stream);
+
+/* data[c, i] /= weight_sum[i] where weight_sum[i] > 1e-8 (data [channels, length] f32).
+ * Replaces chunk_tile::normalize_by_weights (src/chunk_cuda_tile.cu:44-58, 75-83). */
+MBRT_API int mbrt_chunk_normalize(float* data, const float* weight_sum, int64_t channels, int64_t length,
+                                  mbrt_stream_t stream);
+
+/* Fade window of a chunk (host, `chunk_size` floats): ones, with a linear ramp
+ * i / (fade_size - 1) over the first fade_size samples unless `first`, and its mirror over
+ * the last fade_size samples unless `last` (fade_size 1: a single 0 at each faded end).
+ * Requires 2 fade_size <= chunk_size.  Mirrors process_chunked's window
+ * (src/inference_app.cpp:135-148, 201-210).  Host only. */
+MBRT_API int mbrt_chunk_fade_window(float* window, int64_t chunk_size, int64_t fade_size, int first, int last);
+
 /* ---- host-side tables (CPU only, no GPU access) ----------------------------- */
 
 /* Band layout of a MelBandRoformer: the support of a Slaney-normalised mel filterbank

@@ -57,6 +57,7 @@ KERNEL_SOURCES = [
     "k_band.hip",
     "k_attention.hip",
     "k_stft.hip",
+    "k_chunk.hip",
     "host_tables.cpp",
 ]
 
@@ -74,6 +75,7 @@ TENSOR_SOURCES = [
     "tensor_tile.cpp",
     "mbr_tile.cpp",
     "stft_tile.cpp",
+    "chunk_tile.cpp",
 ]
 
 

@@ -499,9 +499,10 @@ __global__ __launch_bounds__(256) void istft_ola_kernel(OlaArgs a) {
             const float* fb = a.frames + (int64_t)b * a.T * kN;
             uint32_t n = sf - tlo * hop;
             for (uint32_t t = tlo; t <= thi; ++t, n -= hop) {
+#pragma clang fp contract(off)
                 acc += fb[(int64_t)t * kN + n];
                 const float wn = a.w[n];
-                ws = __fadd_rn(ws, __fmul_rn(wn, wn));
+                ws = ws + wn * wn;  // squares rounded before the sum, as the oracle's f32 sum
             }
             y = ws > 1.0e-8f ? acc / ws : acc;
         }

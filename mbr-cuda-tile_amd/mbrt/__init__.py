@@ -379,6 +379,32 @@ def istft(spec: torch.Tensor, window: torch.Tensor, hop: int, center: bool = Tru
     return out
 
 
+def chunk_accumulate(dest: torch.Tensor, weight_sum: torch.Tensor, src: torch.Tensor, window: torch.Tensor,
+                     offset: int, stream=None) -> torch.Tensor:
+    """dest [.., L] += src [.., n] * window at `offset` (channels = src.numel() / n); weight_sum += window."""
+    _contig(dest, weight_sum, src, window)
+    n, L = src.shape[-1], dest.shape[-1]
+    _abi.call("mbrt_chunk_accumulate", _p(dest), _p(weight_sum), _p(src), _p(window), src.numel() // max(n, 1), n, L,
+              offset, _s(stream))
+    return dest
+
+
+def chunk_normalize(data: torch.Tensor, weight_sum: torch.Tensor, stream=None) -> torch.Tensor:
+    _contig(data, weight_sum)
+    L = data.shape[-1]
+    _abi.call("mbrt_chunk_normalize", _p(data), _p(weight_sum), data.numel() // max(L, 1), L, _s(stream))
+    return data
+
+
+def chunk_fade_window(chunk_size: int, fade_size: int, first: bool = False, last: bool = False):
+    """Host fade window (numpy f32 [chunk_size])."""
+    import numpy as np
+
+    w = np.empty(chunk_size, dtype=np.float32)
+    _abi.call("mbrt_chunk_fade_window", w.ctypes.data_as(C.c_void_p), chunk_size, fade_size, int(first), int(last))
+    return w
+
+
 # ---- host-side tables -----------------------------------------------------------------------
 
 def mel_band_layout(sample_rate: float = 44100.0, n_fft: int = 2048, n_bands: int = 60, channels: int = 2):

@@ -102,6 +102,9 @@ SIGNATURES: dict[str, list] = {
     "mbrt_istft_output_length": [L, L, I, L],
     "mbrt_istft_workspace_bytes": [L, L],
     "mbrt_istft": [P, I, P, P, L, L, L, L, L, L, L, I, I, L, P, L, P],
+    "mbrt_chunk_accumulate": [P, P, P, P, L, L, L, L, P],
+    "mbrt_chunk_normalize": [P, P, L, L, P],
+    "mbrt_chunk_fade_window": [P, L, L, I, I],
     "mbrt_mel_band_layout": [D, I, I, I, P, L, C.POINTER(C.c_int64), P],
     "mbrt_band_csr": [P, L, L, P, P, P, P],
     "mbrt_rotary_tables": [P, P, L, L, Fl],

@@ -461,3 +461,106 @@ def istft_den(spec, dt, window, hop: int, center: bool = True, normalized: bool 
         d[:, t * hop: t * hop + N_FFT] += M[:, t:t + 1] * w[None, :]
     ws = _window_sum_f32(window, T, hop)
     return _finish(d, ws, T, hop, center, length)
+
+
+# ---- chunk overlap-add (src/chunk_cuda_tile.cu, src/inference_app.cpp:72-232) --------------
+# Restated in numpy float32 with the reference's rounding steps (a rounded product added to
+# a rounded sum), so an ordered evaluation is reproduced bit for bit.
+
+def chunk_fade_window(chunk_size: int, fade_size: int, first: bool = False, last: bool = False) -> np.ndarray:
+    """src/inference_app.cpp:135-148, 201-210: ones with linear ramps i / (fade - 1) (f32)."""
+    w = np.ones(chunk_size, np.float32)
+    if fade_size == 1:
+        if not first:
+            w[0] = 0.0
+        if not last:
+            w[-1] = 0.0
+    elif fade_size > 1:
+        alpha = (np.arange(fade_size, dtype=np.float32) / np.float32(fade_size - 1)).astype(np.float32)
+        if not first:
+            w[:fade_size] = alpha
+        if not last:
+            w[chunk_size - fade_size:] = (np.float32(1.0) - alpha).astype(np.float32)
+    return w
+
+
+def chunk_accumulate(dest: np.ndarray, wsum: np.ndarray, src: np.ndarray, win: np.ndarray, offset: int) -> None:
+    """src/chunk_cuda_tile.cu:18-42, in place: dest[c, off + i] += src[c, i] w[i]; wsum += w."""
+    n = src.shape[-1]
+    d = dest.reshape(-1, dest.shape[-1])
+    s = np.asarray(src, np.float32).reshape(-1, n)
+    w = np.asarray(win, np.float32)
+    d[:, offset:offset + n] = (d[:, offset:offset + n] + (s * w).astype(np.float32)).astype(np.float32)
+    wsum[offset:offset + n] = (wsum[offset:offset + n] + w).astype(np.float32)
+
+
+def chunk_normalize(data: np.ndarray, wsum: np.ndarray) -> None:
+    """src/chunk_cuda_tile.cu:44-58, in place: data /= wsum where wsum > 1e-8 (f32 division)."""
+    d = data.reshape(-1, data.shape[-1])
+    ok = wsum > np.float32(1e-8)
+    q = np.divide(d, np.where(ok, wsum, np.float32(1.0))[None, :]).astype(np.float32)
+    d[:] = np.where(ok[None, :], q, d)
+
+
+def _reflect_pad_last(x: np.ndarray, before: int, after: int) -> np.ndarray:
+    L = x.shape[-1]
+    c = np.arange(-before, L + after)
+    c = np.where(c < 0, -c, c)
+    c = np.where(c >= L, 2 * (L - 1) - c, c)
+    return x[..., np.clip(c, 0, L - 1)]
+
+
+def process_chunked(audio: np.ndarray, chunk_size: int, step: int, chunk_batch_size: int, model_forward):
+    """src/inference_app.cpp:72-232 step for step (model_forward: numpy [G, C, chunk] ->
+    [G, ..., chunk]); audio [1, C, L] f32."""
+    mix = np.asarray(audio, np.float32)
+    length_init = mix.shape[-1]
+    fade_size = chunk_size // 10
+    border = chunk_size - step
+    padded = length_init > 2 * border and border > 0
+    if padded:
+        mix = _reflect_pad_last(mix, border, border)
+    total = mix.shape[-1]
+    starts = list(range(0, total, step))
+    count = len(starts)
+    eff = max(1, min(chunk_batch_size, count))
+
+    def prep(start, end):
+        ch = mix[..., start:end]
+        n = end - start
+        if n < chunk_size:
+            if n > chunk_size // 2:
+                ch = _reflect_pad_last(ch, 0, chunk_size - n)
+            else:
+                ch = np.concatenate([ch, np.zeros(ch.shape[:-1] + (chunk_size - n,), np.float32)], axis=-1)
+        return ch
+
+    def group(g0, gs):
+        ins = [prep(s, min(s + chunk_size, total)) for s in starts[g0:g0 + gs]]
+        return np.asarray(model_forward(np.concatenate(ins, axis=0)), np.float32)
+
+    first = group(0, min(eff, count))
+    out_shape = (1,) + first.shape[1:-1] + (total,)
+    fade = chunk_fade_window(chunk_size, fade_size)
+    out = np.zeros(out_shape, np.float32)
+    wsum = np.zeros(total, np.float32)
+    C = out.size // total
+    out2 = out.reshape(C, total)
+    for g0 in range(0, count, eff):
+        gs = min(eff, count - g0)
+        bo = first if g0 == 0 else group(g0, gs)
+        for local in range(gs):
+            s = starts[g0 + local]
+            e = min(s + chunk_size, total)
+            n = e - s
+            last = e >= total
+            co = bo[local:local + 1][..., :n].reshape(C, n)
+            win = fade
+            if fade_size > 0 and (s == 0 or last):
+                win = chunk_fade_window(chunk_size, fade_size, s == 0, last)
+            chunk_accumulate(out2, wsum, co, win[:n], s)
+    chunk_normalize(out2, wsum)
+    out = out2.reshape(out_shape)
+    if padded:
+        out = out[..., border:border + length_init]
+    return np.ascontiguousarray(out)

@@ -20,6 +20,7 @@
 #include "hip_context.h"
 #include "mbr_tile.h"
 #include "stft_tile.h"
+#include "chunk_tile.h"
 #include "memory_pool.h"
 #include "tensor.h"
 
@@ -330,6 +331,24 @@ void ops(const std::string& path) {
             threw = std::string(e.what()) == "custom STFT only supports n_fft=2048, win_length=2048";
         }
         if (!threw) throw std::runtime_error("stft_tile::stft accepted n_fft=1024");
+    }
+    {
+        namespace K = cudasep::chunk_tile;
+        auto identity = [](const Tensor& x) { return x.clone(); };
+        auto two_stems = [](const Tensor& x) {  // [G, C, n] -> [G, 2, C, n] = (2x, -x)
+            Tensor a = x.clone(), b = x.clone();
+            a.mul_scalar_(2.0f);
+            b.mul_scalar_(-1.0f);
+            return Tensor::stack({a, b}, 1);
+        };
+        std::vector<std::string> log;
+        auto logger = [&log](const std::string& m) { log.push_back(m); };
+        d.save("chunk_a_b1", K::process_chunked(I["audio_a"], 4000, 3000, 1, identity));
+        d.save("chunk_a_b4", K::process_chunked(I["audio_a"], 4000, 3000, 4, identity, logger));
+        d.save("chunk_b_2stem", K::process_chunked(I["audio_b"], 4000, 3200, 2, two_stems));
+        d.save("chunk_c_short", K::process_chunked(I["audio_c"], 4000, 3000, 3, identity));
+        if (log.empty() || log.front() != "[chunk] start" || log.back() != "[chunk] merge complete")
+            throw std::runtime_error("chunk_tile::process_chunked: unexpected log lines");
     }
     cudasep::g_quantize_bf16 = false;
     cudasep::HipContext::instance().synchronize();

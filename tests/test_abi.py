@@ -119,3 +119,17 @@ def test_host_tables_match_oracle(lib, orc):
     assert np.array_equal(c, oc) and np.array_equal(s, os_)
     with pytest.raises(mbrt.MbrtError):
         mbrt.band_csr(np.array([0, 5000], np.int32), 2050)
+
+
+def test_chunk_fade_window_matches_oracle(lib, orc):
+    import numpy as np
+
+    import mbrt
+
+    for n, f in ((524288, 52428), (4000, 400), (7, 1), (7, 0), (10, 5)):
+        for first in (False, True):
+            for last in (False, True):
+                assert np.array_equal(mbrt.chunk_fade_window(n, f, first, last), orc.chunk_fade_window(n, f, first, last))
+    null = C.c_void_p(0)
+    assert lib.mbrt_chunk_fade_window(null, 10, 6, 0, 0) == 3   # fades overlap
+

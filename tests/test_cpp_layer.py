@@ -55,6 +55,8 @@ API = [
     "cudasep::mbr_tile::norm_gamma_bf16_enabled(", "cudasep::mbr_tile::bands_per_freq_bf16_enabled(",
     "cudasep::mbr_tile::rotary_freqs_bf16_enabled(", "cudasep::mbr_tile::scaled_dot_product_attention(",
     "cudasep::stft_tile::hann_window(", "cudasep::stft_tile::stft(", "cudasep::stft_tile::istft(",
+    "cudasep::chunk_tile::accumulate_chunk(", "cudasep::chunk_tile::normalize_by_weights(",
+    "cudasep::chunk_tile::process_chunked(",
     "cudasep::HipMemoryPool::allocate(",
     "cudasep::HipMemoryPool::deallocate(", "cudasep::HipMemoryPool::trim_cached_memory(",
 ]
@@ -129,6 +131,9 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
     m0 = orc.randn((Bb, T, J * 2), seed=rng_seed, stream=14, std=0.5)
     m1 = orc.randn((Bb, T, J * 2), seed=rng_seed, stream=15, std=0.5)
     signal = orc.randn((2, 5000), seed=rng_seed, stream=16)
+    audio_a = orc.randn((1, 2, 16000), seed=rng_seed, stream=17)
+    audio_b = orc.randn((1, 2, 17001), seed=rng_seed, stream=18)
+    audio_c = orc.randn((1, 2, 1500), seed=rng_seed, stream=19)
     cnt = mb["bands_per_freq"].astype(np.float32)
 
     man: list[str] = []
@@ -137,6 +142,7 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
                           ("logits", logits, F32), ("gates", gates, F32), ("q", q, BF16), ("k", k, BF16),
                           ("cos", cos, F32), ("sin", sin, F32), ("qkv", qkv, BF16), ("stft", stft, F32),
                           ("mask0", m0, F32), ("mask1", m1, F32), ("counts", cnt, F32), ("signal", signal, F32),
+                          ("audio_a", audio_a, F32), ("audio_b", audio_b, F32), ("audio_c", audio_c, F32),
                           ("freq_indices", mb["freq_indices"].astype(np.int64), I64),
                           ("csr_off", mb["csr_offsets"].astype(np.int64), I64),
                           ("csr_ind", mb["csr_indices"].astype(np.int64), I64)]:
@@ -209,3 +215,12 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
     dt, y = _read(tmp_path, "istft_bf16")
     assert dt == F32 and y.shape == (2, 11 * 441)
     assert_close(y, orc.istft(sb, BF16, hw, 441), F32, "stft_tile::istft bf16", den=orc.istft_den(sb, BF16, hw, 441))
+    ident = lambda a: a.copy()
+    for name, ref in (("chunk_a_b1", orc.process_chunked(audio_a, 4000, 3000, 1, ident)),
+                      ("chunk_a_b4", orc.process_chunked(audio_a, 4000, 3000, 4, ident)),
+                      ("chunk_b_2stem", orc.process_chunked(audio_b, 4000, 3200, 2,
+                                                            lambda a: np.stack([2 * a, -a], axis=1))),
+                      ("chunk_c_short", orc.process_chunked(audio_c, 4000, 3000, 3, ident))):
+        dt, y = _read(tmp_path, name)
+        assert dt == F32
+        assert_bitexact(y, ref, f"chunk_tile::process_chunked {name}")
