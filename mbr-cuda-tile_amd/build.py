@@ -76,6 +76,7 @@ TENSOR_SOURCES = [
     "mbr_tile.cpp",
     "stft_tile.cpp",
     "chunk_tile.cpp",
+    "weights.cpp",
 ]
 
 

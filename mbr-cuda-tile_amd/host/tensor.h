@@ -129,6 +129,8 @@ public:
     std::string shape_str() const;
 
 private:
+    friend class ModelWeights;  // builds its tensors as views into one weight arena
+
     std::shared_ptr<void> storage_;  // device memory from HipMemoryPool
     void* data_;                     // first element (views point into storage_)
     std::vector<int64_t> shape_;

@@ -21,6 +21,7 @@
 #include "mbr_tile.h"
 #include "stft_tile.h"
 #include "chunk_tile.h"
+#include "weights.h"
 #include "memory_pool.h"
 #include "tensor.h"
 
@@ -354,6 +355,126 @@ void ops(const std::string& path) {
     cudasep::HipContext::instance().synchronize();
 }
 
+// ---- csm mode: .csm loader, JSON, band tables --------------------------------------------
+
+void json_dump(std::ostream& o, const cudasep::JsonValue& v) {
+    using J = cudasep::JsonValue;
+    switch (v.type()) {
+        case J::Null: o << "null"; break;
+        case J::Bool: o << (v.as_bool() ? "true" : "false"); break;
+        case J::Number: {
+            char b[64];
+            std::snprintf(b, sizeof b, "%.17g", v.as_number());
+            o << b;
+            break;
+        }
+        case J::String: {
+            o << '"';
+            for (unsigned char c : v.as_string()) {
+                if (c == '"' || c == '\\') o << '\\' << c;
+                else if (c < 0x20) {
+                    char b[8];
+                    std::snprintf(b, sizeof b, "\\u%04x", c);
+                    o << b;
+                } else o << c;
+            }
+            o << '"';
+            break;
+        }
+        case J::Array:
+            o << '[';
+            for (size_t i = 0; i < v.size(); ++i) {
+                if (i) o << ',';
+                json_dump(o, v[i]);
+            }
+            o << ']';
+            break;
+        case J::Object: {
+            o << '{';
+            bool first = true;
+            for (const auto& k : v.keys()) {
+                if (!first) o << ',';
+                first = false;
+                json_dump(o, J::make_string(k));
+                o << ':';
+                json_dump(o, v[k]);
+            }
+            o << '}';
+            break;
+        }
+    }
+}
+
+void csm(const std::string& path) {
+    using cudasep::ModelWeights;
+    Dir d{path, {}};
+    // JSON cases, one per line: canonical dump or "ERR <message>"
+    {
+        std::ifstream in(path + "/json_cases.txt");
+        std::ofstream out(path + "/json_out.txt");
+        std::string line;
+        while (std::getline(in, line)) {
+            try {
+                json_dump(out, cudasep::JsonValue::parse(line));
+            } catch (const std::exception& e) {
+                out << "ERR " << e.what();
+            }
+            out << "\n";
+        }
+    }
+    // a model file: tensors in sorted-name order, the config, band tables, bf16 conversion
+    ModelWeights w = ModelWeights::load(path + "/model.csm");
+    {
+        std::ofstream names(path + "/names.txt");
+        int i = 0;
+        for (const auto& n : w.tensor_names()) {
+            names << n << "\n";
+            d.save("t" + std::to_string(i++), w.get(n));
+        }
+        std::ofstream cfg(path + "/config_out.txt");
+        json_dump(cfg, w.config());
+        cfg << "\n" << w.config().get_int("num_bands", -1) << " " << w.config().get_int("missing", 7) << " "
+            << w.config().get_float("stft_hop_length", -1.f) << " " << w.config().get_bool("stereo", false) << " "
+            << w.config().get_string("model_type", "none") << "\n";
+        check(w.arena_bytes() % 256 == 0, "arena is a multiple of 256 bytes");
+        bool threw = false;
+        try {
+            (void)w.get("no.such.tensor");
+        } catch (const std::runtime_error& e) {
+            threw = std::string(e.what()) == "ModelWeights: tensor not found: no.such.tensor";
+        }
+        check(threw, "get() of a missing tensor throws the reference's message");
+    }
+    if (w.has("__precomputed__.freq_indices")) {
+        const auto& c = w.config();
+        cudasep::MelBandTables t = cudasep::load_mel_band_tables(w, c.get_int("num_bands", 60),
+                                                                 c.get_int("stft_n_fft", 2048), c.get_bool("stereo", true));
+        d.save("band_offsets", t.freq_band_offsets);
+        d.save("band_indices", t.freq_band_indices);
+        d.save("band_counts", t.num_bands_per_freq);
+        std::ofstream o(path + "/band_dims.txt");
+        o << t.max_bands_per_freq;
+        for (int64_t x : t.band_freq_dims) o << " " << x;
+        o << "\n";
+    }
+    w.convert_linear_weights_to_bf16();
+    {
+        int i = 0;
+        for (const auto& n : w.tensor_names()) d.save("c" + std::to_string(i++), w.get(n));
+    }
+    // malformed files: each load must throw; the message is recorded
+    std::ofstream errs(path + "/errors.txt");
+    for (const char* bad : {"bad_magic", "bad_version", "truncated", "bad_dtype", "missing"}) {
+        try {
+            (void)ModelWeights::load(path + "/" + bad + ".csm");
+            errs << bad << " LOADED\n";
+        } catch (const std::exception& e) {
+            errs << bad << " " << e.what() << "\n";
+        }
+    }
+    cudasep::HipContext::instance().synchronize();
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -361,8 +482,9 @@ int main(int argc, char** argv) {
     try {
         if (mode == "unit") unit();
         else if (mode == "ops" && argc > 2) ops(argv[2]);
+        else if (mode == "csm" && argc > 2) csm(argv[2]);
         else {
-            std::cerr << "usage: tensor_selftest unit | ops <dir>" << std::endl;
+            std::cerr << "usage: tensor_selftest unit | ops <dir> | csm <dir>" << std::endl;
             return 2;
         }
     } catch (const std::exception& e) {

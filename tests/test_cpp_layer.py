@@ -100,7 +100,7 @@ def _write(dirp: Path, manifest: list, name: str, arr: np.ndarray, dt: int):
 def _read(dirp: Path, name: str):
     meta = (dirp / f"{name}.meta").read_text().split()
     dt, shape = int(meta[0]), tuple(int(s) for s in meta[1:])
-    np_dt = {F32: np.float32, BF16: np.uint16}[dt]
+    np_dt = {F32: np.float32, BF16: np.uint16, 1: np.uint16, I64: np.int64}[dt]
     return dt, np.fromfile(dirp / f"{name}.out", dtype=np_dt).reshape(shape)
 
 
@@ -224,3 +224,93 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
         dt, y = _read(tmp_path, name)
         assert dt == F32
         assert_bitexact(y, ref, f"chunk_tile::process_chunked {name}")
+
+
+JSON_CASES = [
+    '{"a": 1, "b": [1, 2.5e-3, -0.0, 1E+2], "c": {"d": null, "e": true, "f": false}}',
+    '"esc \\" \\\\ \\/ \\b\\f\\n\\r\\t \\u00e9 \\ud83d\\ude00"',
+    '[]', '{}', '  [ 0 , -1 , 123456789012 ]  ', '3.141592653589793', '"naïve"',
+    '{"a": 1,}', '[1 2]', '{"a" 1}', 'tru', '"unterminated', '01', '[1] x', '',
+]
+
+
+@pytest.mark.gpu
+def test_csm_loader_json_and_band_tables(orc, dev, tmp_path):
+    """ModelWeights::load against files written by mbrt.csm: every tensor bit-exact (all
+    dtypes, 0-d, empty, a repeated name whose last copy wins), the config through the JSON
+    parser, the bf16 conversion of 2-D f32 tensors, the band tables MelBandRoformer::load
+    builds from __precomputed__ tensors, and the reference's errors for malformed files."""
+    import json
+    import struct
+
+    from mbrt import csm
+
+    rng = np.random.default_rng(31)
+    cfg = {"num_bands": 60, "stft_n_fft": 2048, "stereo": True, "stft_hop_length": 441,
+           "model_type": "mel_band_roformer", "dims": [384, 1536], "nested": {"x": [1.5, None, "s"]}}
+    items = [("layers.0.w", rng.standard_normal((384, 1536)).astype(np.float32)),
+             ("layers.0.b", rng.standard_normal(1536).astype(np.float32)),
+             ("half", rng.standard_normal((7, 3)).astype(np.float16)),
+             ("bf", rng.integers(0, 2**16, size=(5, 9)).astype(np.uint16)),
+             ("idx", np.arange(-5, 6, dtype=np.int64)),
+             ("scalar", np.array(-3.25, np.float32)), ("empty", np.zeros((0, 8), np.float32)),
+             ("dup", np.zeros(3, np.float32)), ("dup", np.arange(3, dtype=np.float32))]
+    items += list(csm.precomputed_band_tensors(44100.0, 2048, 60, True).items())
+    csm.write_csm(tmp_path / "model.csm", cfg, items, dtypes={"bf": csm.BF16})
+    good = (tmp_path / "model.csm").read_bytes()
+    (tmp_path / "bad_magic.csm").write_bytes(b"CSN\x00" + good[4:])
+    (tmp_path / "bad_version.csm").write_bytes(good[:4] + struct.pack("<I", 3) + good[8:])
+    (tmp_path / "truncated.csm").write_bytes(good[:-10])
+    csm.write_csm(tmp_path / "bad_dtype.csm", {}, [("w", np.ones(2, np.float32))])
+    bd = bytearray((tmp_path / "bad_dtype.csm").read_bytes())
+    struct.pack_into("<I", bd, len(bd) - 8 - 4, 9)  # dtype field of the only tensor
+    (tmp_path / "bad_dtype.csm").write_bytes(bytes(bd))
+    (tmp_path / "json_cases.txt").write_text("\n".join(JSON_CASES) + "\n", encoding="utf-8")
+
+    r = _selftest("csm", str(tmp_path))
+    print(r.stdout[-3000:])
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+
+    want = {}
+    for n, a in items:
+        want[n] = a
+    names = (tmp_path / "names.txt").read_text(encoding="utf-8").splitlines()
+    assert names == sorted(want)
+    for i, n in enumerate(names):
+        dt, y = _read(tmp_path, f"t{i}")
+        assert y.shape == want[n].shape, n
+        assert_bitexact(y, want[n].view(y.dtype) if want[n].dtype.itemsize == y.dtype.itemsize else want[n], n)
+        # after convert_linear_weights_to_bf16: 2-D f32 -> bf16 (RNE), the rest unchanged
+        cdt, c = _read(tmp_path, f"c{i}")
+        if want[n].ndim == 2 and want[n].dtype == np.float32:
+            assert cdt == BF16
+            assert_bitexact(c, orc.f32_to_bf16(want[n]), f"{n} as bf16")
+        else:
+            assert cdt == dt
+            assert_bitexact(c, y, f"{n} unchanged")
+    lines = (tmp_path / "config_out.txt").read_text(encoding="utf-8").splitlines()
+    assert json.loads(lines[0]) == cfg
+    assert lines[1].split() == ["60", "7", "441", "1", "mel_band_roformer"]
+    mb = orc.mel_bands(44100.0, 2048, 60, 2)
+    assert_bitexact(_read(tmp_path, "band_offsets")[1], mb["csr_offsets"].astype(np.int64), "band CSR offsets")
+    assert_bitexact(_read(tmp_path, "band_indices")[1], mb["csr_indices"].astype(np.int64), "band CSR indices")
+    assert_bitexact(_read(tmp_path, "band_counts")[1], mb["bands_per_freq"].astype(np.float32), "bands per freq")
+    dims = [int(v) for v in (tmp_path / "band_dims.txt").read_text().split()]
+    assert dims[0] == 2 and dims[1:] == (4 * mb["freqs_per_band"]).tolist()
+    errs = dict(ln.split(" ", 1) for ln in (tmp_path / "errors.txt").read_text().splitlines())
+    assert errs["bad_magic"] == "ModelWeights: invalid magic (expected CSM\\0)"
+    assert errs["bad_version"] == "ModelWeights: unsupported version 3"
+    assert errs["truncated"].startswith("ModelWeights: unexpected EOF")
+    assert errs["bad_dtype"] == "ModelWeights: unknown dtype 9 for tensor w"
+    assert errs["missing"].startswith("ModelWeights: cannot open file: ")
+    outs = (tmp_path / "json_out.txt").read_text(encoding="utf-8").splitlines()
+    assert len(outs) == len(JSON_CASES)
+    for case, out in zip(JSON_CASES, outs):
+        try:
+            ref = json.loads(case)
+        except ValueError:
+            assert out.startswith("ERR JSON parse error at position"), (case, out)
+            continue
+        assert not out.startswith("ERR"), (case, out)
+        assert json.loads(out) == ref, (case, out)
+
