@@ -118,7 +118,7 @@ def build_ops(torch, mbrt, bands):
             op = Op(f"bl3_softmax_{tag}_{dname}", 2 * rows * cols * es,
                     (lambda rows=rows, cols=cols, dt=dt: dict(x=randn((rows, cols), dt, 3.0),
                                                               y=torch.empty((rows, cols), dtype=dt, device=dev))),
-                    "softmax_rows_kernel" if tag == "time" else "softmax_staged_kernel")
+                    "softmax_staged_kernel")  # rows of up to 1024 elements are staged through LDS
             op.run = lambda b: mbrt.softmax(b["x"], b["y"], 1.0)
             ops.append(op)
 
