@@ -72,7 +72,7 @@ __device__ __forceinline__ float xor_sum(float x) {
 // QS = 16-query sub-blocks per wave (1 or 2): every K and V^T fragment read from LDS
 // feeds QS MFMAs, so longer sequences use QS = 2 (128 queries per workgroup).
 template <int ODT, int QS>
-__global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) __bf16 ks[kKeys][kHeadDim + kPad];   // K tile [key][d]
     __shared__ __attribute__((aligned(16))) __bf16 vs[kKeys][kHeadDim + kPad];   // V tile [key][d]
     constexpr int kQB = kQWave * QS * kWaves;  // queries per workgroup
@@ -108,13 +108,14 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs a) {
     // is fetched into registers while the current one is computed from LDS.
     // Thread t stages the 16-byte vectors t and t + 256 (key = vector / 8) of each tile.
     bf16x8 kv[2], vv[2];
+    // element offsets within one (b, h) fit 32 bits (n_k * 64 < 2^31 is checked on the host)
     auto fetch = [&](int kt) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int vec = tid + 256 * u, dc = (vec & 7) * 8;
-            const int64_t row = min(kt + (vec >> 3), a.nk - 1);
-            kv[u] = *reinterpret_cast<const bf16x8*>(kbase + row * kHeadDim + dc);
-            vv[u] = *reinterpret_cast<const bf16x8*>(vbase + row * kHeadDim + dc);
+            const uint32_t off = (uint32_t)min(kt + (vec >> 3), a.nk - 1) * kHeadDim + dc;
+            kv[u] = *reinterpret_cast<const bf16x8*>(kbase + off);
+            vv[u] = *reinterpret_cast<const bf16x8*>(vbase + off);
         }
     };
     fetch(0);
@@ -164,12 +165,16 @@ __global__ __launch_bounds__(kWaves * 64) void attention_kernel(AttnArgs a) {
             for (int kb = 0; kb < 4; ++kb)
                 mx = fmaxf(mx, fmaxf(fmaxf(st[x][kb][0], st[x][kb][1]), fmaxf(st[x][kb][2], st[x][kb][3])));
             mx = xor_max(mx) * a.scale_log2e;
-            if (mx > m[x] + kLazy) {
-                const float alpha = __builtin_amdgcn_exp2f(m[x] - mx);
+            // wave-uniform branch: the rescale runs only on the (rare) tiles where some query
+            // of the wave outgrows its reference; queries that do not keep alpha = 1
+            const bool grow = mx > m[x] + kLazy;
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+                const float mn = grow ? mx : m[x];
+                const float alpha = __builtin_amdgcn_exp2f(m[x] - mn);
                 l[x] *= alpha;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) o[x][db] *= alpha;
-                m[x] = mx;
+                m[x] = mn;
             }
             float psum = 0.0f;
 #pragma unroll
@@ -263,7 +268,7 @@ int mbrt_attention(const void* q, const void* k, const void* v, int dtype, void*
     MBRT_REQUIRE(BH >= 0 && n_q >= 0 && n_k >= 0, MBRT_E_SHAPE, "%s: bad shape", op);
     if (BH == 0 || n_q == 0) return MBRT_OK;
     MBRT_REQUIRE(n_k >= 1, MBRT_E_SHAPE, "%s: attention over zero keys", op);
-    MBRT_REQUIRE(n_q < (1 << 30) && n_k < (1 << 30), MBRT_E_SHAPE, "%s: shape too large", op);
+    MBRT_REQUIRE(n_q < (1 << 24) && n_k < (1 << 24), MBRT_E_SHAPE, "%s: sequence longer than 2^24", op);
     MBRT_REQUIRE(q && k && v && out, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
     MBRT_REQUIRE(scale >= 0.0f && std::isfinite(scale), MBRT_E_INVALID_ARG, "%s: scale must be finite and >= 0", op);
     MBRT_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16), MBRT_E_ALIGN,
