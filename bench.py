@@ -184,8 +184,8 @@ def build_ops(torch, mbrt, bands):
     for stag, sdt, ssz in (("f32", torch.float32, 4), ("bf16", bf16, 2)):
         op = Op(f"istft_chunk_{stag}", Bs * 1025 * Ts * 2 * ssz + 2048 * 4 + Bs * Ls * 4,
                 (lambda sdt=sdt: dict(s=randn((Bs, 1025, Ts, 2), sdt), y=torch.empty((Bs, Ls), device=dev),
-                                      w=torch.empty(Bs * Ts * 2048, device=dev))),
-                "istft_frames_kernel")
+                                      w=torch.empty(mbrt.istft_workspace_bytes(Bs, Ts, 441) // 4, device=dev))),
+                "istft_block_kernel")
         op.next = True
         op.run = lambda b: mbrt.istft(b["s"], win, 441, length=Ls, out=b["y"], workspace=b["w"])
         ops.append(op)

@@ -354,16 +354,19 @@ MBRT_API int mbrt_stft(const float* signal, const float* window, float* out, int
  * when centred.  -1 for frames < 1 or hop < 1.  Host only. */
 MBRT_API int64_t mbrt_istft_output_length(int64_t frames, int64_t hop, int center, int64_t length);
 
-/* Workspace mbrt_istft needs: batch * frames * 2048 f32 (the windowed frames). */
-MBRT_API int64_t mbrt_istft_workspace_bytes(int64_t batch, int64_t frames);
+/* Workspace mbrt_istft needs, in bytes: the overlap-added partial signal of every block of
+ * 8 frames, batch * ceil(frames / 8) * (7 hop + 2048) f32.  -1 for a negative extent or a
+ * hop outside 1..2^20. */
+MBRT_API int64_t mbrt_istft_workspace_bytes(int64_t batch, int64_t frames, int64_t hop);
 
 /* Inverse STFT of spec [batch, 1025, frames, 2] (F32 or BF16; times sqrt(2048) when
  * normalized): each frame is the real inverse DFT (imaginary parts of bins 0 and 1024
  * ignored) times the window, overlap-added at hop spacing and divided by the window's
  * summed squares where that sum exceeds 1e-8; centred output drops 1024 samples at each
  * end; `length` > 0 trims or zero-fills to that length.  out is [batch,
- * mbrt_istft_output_length(...)] f32.  Frames are summed per sample in frame order (the
- * reference adds them with atomics).  Replaces stft_tile::istft
+ * mbrt_istft_output_length(...)] f32.  Frames are summed per sample in frame order within
+ * blocks of 8, then the block sums in block order (the reference adds them with atomics),
+ * so the result is deterministic.  hop <= 2^20.  Replaces stft_tile::istft
  * (src/stft_cuda_tile.cu:600-717). */
 MBRT_API int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out, int64_t batch,
                         int64_t freq_bins, int64_t frames, int64_t n_fft, int64_t hop, int64_t win_length,

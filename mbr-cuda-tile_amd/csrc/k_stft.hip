@@ -389,12 +389,21 @@ __global__ __launch_bounds__(64 * TF) void stft_kernel(StftArgs a) {
 }
 
 // ---- iSTFT ------------------------------------------------------------------------------
-struct IstftFramesArgs {
+// Block kernel: one workgroup = kTF consecutive frames of one signal.  Their spectra are
+// loaded transposed, each wave inverts one frame and leaves it, windowed and scaled, in its
+// LDS slot; the workgroup then overlap-adds its frames in LDS (frame order) and writes the
+// block's partial signal, (nf - 1) hop + 2048 samples from sample t0 hop.  The final
+// kernel adds, per output sample, the partials of the blocks that cover it (block order)
+// and divides by the window sum.
+struct IstftBlockArgs {
     const void* spec;   // [B, 1025, T] complex, f32 or bf16
     const float* w;
-    float* frames;      // [B*T, 2048]
-    uint32_t frames_n;  // B * T
-    FastDiv T;
+    float* part;        // [B, nTB, span] block partials
+    uint32_t T;
+    FastDiv ntb;        // blocks per signal
+    FastDiv hop;
+    uint32_t span;      // (kTF - 1) hop + 2048: stride of a block's partial
+    uint32_t blocks;    // B * nTB
     int wvec;           // window is 8-byte aligned
     float spec_scale;
 };
@@ -410,20 +419,21 @@ __device__ __forceinline__ float2 load_bin(const void* spec, int64_t i) {
 }
 
 template <int TF, int SDT>
-__global__ __launch_bounds__(64 * TF) void istft_frames_kernel(IstftFramesArgs a) {
+__global__ __launch_bounds__(64 * TF) void istft_block_kernel(IstftBlockArgs a) {
     constexpr int NT = 64 * TF;
     __shared__ __attribute__((aligned(16))) float2 lds[TF * kSlot + kTwSlots];
     float2* tw = lds + TF * kSlot;
-    const uint32_t g0 = xcd_runs<kXcdRun>(blockIdx.x, gridDim.x) * TF;
+    const uint32_t blk = xcd_runs<kXcdRun>(blockIdx.x, gridDim.x);
+    uint32_t b, tb;
+    fdivmod(blk, a.ntb, b, tb);
+    const uint32_t t0 = tb * TF;
+    const uint32_t nf = min((uint32_t)TF, a.T - t0);
     {
         // transposed spectrum load: thread -> (frame tl, bins fr, fr + 64, ...)
         const int tl = threadIdx.x % TF, fr = threadIdx.x / TF;
-        const uint32_t g = g0 + tl;
-        if (g < a.frames_n) {
-            uint32_t b, t;
-            fdivmod(g, a.T, b, t);
-            int64_t idx = (int64_t)b * kBins * a.T.d + t + (int64_t)fr * a.T.d;
-            const int64_t step = (int64_t)(NT / TF) * a.T.d;
+        if ((uint32_t)tl < nf) {
+            int64_t idx = (int64_t)b * kBins * a.T + t0 + tl + (int64_t)fr * a.T;
+            const int64_t step = (int64_t)(NT / TF) * a.T;
             float2* slot = lds + tl * kSlot;
 #pragma unroll 4
             for (int f = fr; f < kBins; f += NT / TF, idx += step) {
@@ -435,78 +445,107 @@ __global__ __launch_bounds__(64 * TF) void istft_frames_kernel(IstftFramesArgs a
     load_twiddles<NT>(tw);
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const uint32_t g = g0 + wave;
-    if (g >= a.frames_n) return;
-    float2* slot = lds + wave * kSlot;
-    // inverse real split, in place: (X[k], X[1024 - k]) -> (Z[k], Z[1024 - k]) scaled by 2;
-    // Z[0] from the real parts of X[0] and X[1024] (their imaginary parts drop out).
-    cf x0{0.f, 0.f}, xn{0.f, 0.f};
-    if (lane == 0) {
-        x0 = lds_ld(slot, 0);
-        xn = lds_ld(slot, pad16(kN / 2));
+    if ((uint32_t)wave < nf) {
+        float2* slot = lds + wave * kSlot;
+        // inverse real split, in place: (X[k], X[1024 - k]) -> (Z[k], Z[1024 - k]) scaled by 2;
+        // Z[0] from the real parts of X[0] and X[1024] (their imaginary parts drop out).
+        cf x0{0.f, 0.f}, xn{0.f, 0.f};
+        if (lane == 0) {
+            x0 = lds_ld(slot, 0);
+            xn = lds_ld(slot, pad16(kN / 2));
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int k = 1 + lane + 64 * q, gg = kN / 2 - k;
+            const cf xk = lds_ld(slot, pad16(k)), xg = lds_ld(slot, pad16(gg));
+            const cf A{xk.x + xg.x, xk.y - xg.y}, Bv{xk.x - xg.x, xk.y + xg.y};
+            const cf Q = cmul(Bv, twiddle<true>(tw, k));
+            lds_st(slot, pad16(k), cf{A.x - Q.y, A.y + Q.x});
+            lds_st(slot, pad16(gg), cf{A.x + Q.y, Q.x - A.y});
+        }
+        if (lane == 0) lds_st(slot, 0, cf{x0.x + xn.x, x0.x - xn.x});
+        wave_lds_sync();
+        cf v[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = lds_ld(slot, pad16(lane) + 68 * q);
+        fft1024<true>(v, slot, tw, lane);
+        // lane l holds 2048 * (x[2m], x[2m + 1]), m = l + 64a: the windowed frame goes back into
+        // the slot as 2048 consecutive floats
+        wave_lds_sync();
+        constexpr float kInvN = 1.0f / (float)kN;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int m = lane + 64 * q;
+            float2 w;
+            if (a.wvec) w = reinterpret_cast<const float2*>(a.w)[m];
+            else w = make_float2(a.w[2 * m], a.w[2 * m + 1]);
+            slot[m] = make_float2(v[q].x * w.x * kInvN, v[q].y * w.y * kInvN);
+        }
     }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const int k = 1 + lane + 64 * q, gg = kN / 2 - k;
-        const cf xk = lds_ld(slot, pad16(k)), xg = lds_ld(slot, pad16(gg));
-        const cf A{xk.x + xg.x, xk.y - xg.y}, Bv{xk.x - xg.x, xk.y + xg.y};
-        const cf Q = cmul(Bv, twiddle<true>(tw, k));
-        lds_st(slot, pad16(k), cf{A.x - Q.y, A.y + Q.x});
-        lds_st(slot, pad16(gg), cf{A.x + Q.y, Q.x - A.y});
-    }
-    if (lane == 0) lds_st(slot, 0, cf{x0.x + xn.x, x0.x - xn.x});
-    wave_lds_sync();
-    cf v[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) v[q] = lds_ld(slot, pad16(lane) + 68 * q);
-    fft1024<true>(v, slot, tw, lane);
-    // lane l holds 2048 * (x[2m], x[2m + 1]), m = l + 64a
-    float2* dst = reinterpret_cast<float2*>(a.frames + (int64_t)g * kN);
-    constexpr float kInvN = 1.0f / (float)kN;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int m = lane + 64 * q;
-        float2 w;
-        if (a.wvec) w = reinterpret_cast<const float2*>(a.w)[m];
-        else w = make_float2(a.w[2 * m], a.w[2 * m + 1]);
-        dst[m] = make_float2(v[q].x * w.x * kInvN, v[q].y * w.y * kInvN);
+    __syncthreads();
+    // overlap-add of the block's frames in frame order: partial[u], u = s - t0 hop
+    const uint32_t hop = a.hop.d;
+    const uint32_t span = (nf - 1) * hop + kN;
+    float* part = a.part + (int64_t)blk * a.span;
+    for (uint32_t u = threadIdx.x; u < span; u += NT) {
+        const uint32_t jhi = min(nf - 1, fdiv(u, a.hop));
+        const uint32_t jlo = u >= (uint32_t)kN ? fdiv(u - kN, a.hop) + 1 : 0;
+        float acc = 0.0f;
+        for (uint32_t j = jlo; j <= jhi; ++j) acc += reinterpret_cast<const float*>(lds + j * kSlot)[u - j * hop];
+        part[u] = acc;
     }
 }
 
-struct OlaArgs {
-    const float* frames;  // [B*T, 2048]
+struct IstftFinalArgs {
+    const float* part;    // [B, nTB, span]
     const float* w;
     float* out;           // [B, out_len]
-    uint32_t total;       // B * out_len
-    FastDiv out_len;
+    uint32_t batch;
+    uint32_t out_len;
     FastDiv hop;
-    uint32_t valid;       // samples of the (trimmed) signal; out_len - valid zeros follow
+    FastDiv bhop;         // kTF * hop: block stride in samples
+    uint32_t span;
+    uint32_t ntb;
     uint32_t T;
+    uint32_t valid;       // samples of the (trimmed) signal; out_len - valid zeros follow
     uint32_t offset;      // 1024 when centred
 };
 
-__global__ __launch_bounds__(256) void istft_ola_kernel(OlaArgs a) {
-    const uint32_t hop = a.hop.d;
-    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < a.total; i += gridDim.x * 256) {
-        uint32_t b, s;
-        fdivmod(i, a.out_len, b, s);
-        float y = 0.0f;
-        if (s < a.valid) {
-            const uint32_t sf = s + a.offset;
-            const uint32_t thi = min(a.T - 1, fdiv(sf, a.hop));
-            const uint32_t tlo = sf >= (uint32_t)kN ? fdiv(sf - kN, a.hop) + 1 : 0;
-            float acc = 0.0f, ws = 0.0f;
-            const float* fb = a.frames + (int64_t)b * a.T * kN;
-            uint32_t n = sf - tlo * hop;
-            for (uint32_t t = tlo; t <= thi; ++t, n -= hop) {
-#pragma clang fp contract(off)
-                acc += fb[(int64_t)t * kN + n];
-                const float wn = a.w[n];
-                ws = ws + wn * wn;  // squares rounded before the sum, as the oracle's f32 sum
-            }
-            y = ws > 1.0e-8f ? acc / ws : acc;
+// One thread per output sample position, for every signal of the batch: the window sum
+// (the same for all signals) is formed once.
+__global__ __launch_bounds__(256) void istft_final_kernel(IstftFinalArgs a) {
+    const uint32_t hop = a.hop.d, bhop = a.bhop.d;
+    for (uint32_t so = blockIdx.x * 256 + threadIdx.x; so < a.out_len; so += gridDim.x * 256) {
+        if (so >= a.valid) {
+            for (uint32_t b = 0; b < a.batch; ++b) a.out[(int64_t)b * a.out_len + so] = 0.0f;
+            continue;
         }
-        a.out[i] = y;
+        const uint32_t s = so + a.offset;
+        // window sum of squares in frame order (f32), as the reference's window_sum
+        const uint32_t thi = min(a.T - 1, fdiv(s, a.hop));
+        const uint32_t tlo = s >= (uint32_t)kN ? fdiv(s - kN, a.hop) + 1 : 0;
+        float ws = 0.0f;
+        uint32_t n = s - tlo * hop;
+        for (uint32_t t = tlo; t <= thi; ++t, n -= hop) {
+#pragma clang fp contract(off)
+            const float wn = a.w[n];
+            ws = ws + wn * wn;
+        }
+        // blocks covering s, in block order; a block's partial is shorter when it is the last
+        // one of its signal
+        const uint32_t bhi = min(a.ntb - 1, fdiv(s, a.bhop));
+        const uint32_t blo = s >= a.span ? fdiv(s - a.span, a.bhop) + 1 : 0;
+#pragma unroll 4
+        for (uint32_t b = 0; b < a.batch; ++b) {
+            const float* pb = a.part + (int64_t)b * a.ntb * a.span;
+            float acc = 0.0f;
+            for (uint32_t tb = blo; tb <= bhi; ++tb) {
+                const uint32_t u = s - tb * bhop;
+                const uint32_t nf = min((uint32_t)kTF, a.T - tb * kTF);
+                if (u < (nf - 1) * hop + kN) acc += pb[(int64_t)tb * a.span + u];
+            }
+            a.out[(int64_t)b * a.out_len + so] = ws > 1.0e-8f ? acc / ws : acc;
+        }
     }
 }
 
@@ -524,6 +563,8 @@ int check_fixed_size(const char* op, int64_t n_fft, int64_t win_length, int64_t 
                  (long long)win_length, (long long)window_numel);
     return MBRT_OK;
 }
+
+constexpr int64_t kMaxHop = int64_t(1) << 20;  // keeps block spans and sample indices in 32 bits
 
 int64_t grid_for(int64_t work, int64_t per_block) {
     return std::min<int64_t>(ceil_div(work, per_block), int64_t(1) << 20);
@@ -594,9 +635,9 @@ int64_t mbrt_istft_output_length(int64_t frames, int64_t hop, int center, int64_
     return center ? full - kN : full;
 }
 
-int64_t mbrt_istft_workspace_bytes(int64_t batch, int64_t frames) {
-    if (batch < 0 || frames < 0) return -1;
-    return batch * frames * kN * (int64_t)sizeof(float);
+int64_t mbrt_istft_workspace_bytes(int64_t batch, int64_t frames, int64_t hop) {
+    if (batch < 0 || frames < 0 || hop < 1 || hop > kMaxHop) return -1;
+    return batch * ceil_div(frames, kTF) * ((kTF - 1) * hop + kN) * (int64_t)sizeof(float);
 }
 
 int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out, int64_t batch,
@@ -610,49 +651,54 @@ int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out
                  (long long)freq_bins);
     MBRT_REQUIRE(spec_dtype == F32 || spec_dtype == BF16, MBRT_E_UNSUPPORTED_DTYPE,
                  "%s: spectrum must be F32 or BF16", op);
-    MBRT_REQUIRE(batch >= 0 && frames >= 1 && frames < (1 << 30) && hop >= 1 && hop < (1 << 30), MBRT_E_SHAPE,
+    MBRT_REQUIRE(batch >= 0 && frames >= 1 && frames < (1 << 30) && hop >= 1 && hop <= kMaxHop, MBRT_E_SHAPE,
                  "%s: bad shape (batch %lld, frames %lld, hop %lld)", op, (long long)batch, (long long)frames,
                  (long long)hop);
     const int64_t out_len = mbrt_istft_output_length(frames, hop, center, length);
     if (batch == 0 || out_len == 0) return MBRT_OK;
     MBRT_REQUIRE(spec && window && out && workspace, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
-    MBRT_REQUIRE(workspace_bytes >= mbrt_istft_workspace_bytes(batch, frames), MBRT_E_INVALID_ARG,
-                 "%s: workspace of %lld bytes, %lld needed", op, (long long)workspace_bytes,
-                 (long long)mbrt_istft_workspace_bytes(batch, frames));
-    MBRT_REQUIRE(aligned(workspace, 8) && aligned(spec, spec_dtype == F32 ? 8 : 4), MBRT_E_ALIGN,
-                 "%s: spectrum and workspace must be aligned to their complex element", op);
+    const int64_t need = mbrt_istft_workspace_bytes(batch, frames, hop);
+    MBRT_REQUIRE(workspace_bytes >= need, MBRT_E_INVALID_ARG, "%s: workspace of %lld bytes, %lld needed", op,
+                 (long long)workspace_bytes, (long long)need);
+    MBRT_REQUIRE(aligned(workspace, 4) && aligned(spec, spec_dtype == F32 ? 8 : 4), MBRT_E_ALIGN,
+                 "%s: spectrum and workspace must be aligned to their element", op);
+    const int64_t full = kN + (frames - 1) * hop;
+    const int64_t ntb = ceil_div(frames, kTF);
+    MBRT_REQUIRE(batch * ntb < (int64_t(1) << 31) && batch * out_len < (int64_t(1) << 31) &&
+                     full + kN < (int64_t(1) << 31),
+                 MBRT_E_SHAPE, "%s: signal too long", op);
     hipStream_t st = as_stream(stream);
-    IstftFramesArgs fa{};
-    fa.spec = spec;
-    fa.w = window;
-    fa.frames = static_cast<float*>(workspace);
-    MBRT_REQUIRE(batch * frames < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many frames", op);
-    fa.frames_n = (uint32_t)(batch * frames);
-    fa.T = make_fastdiv((uint32_t)frames);
-    fa.spec_scale = normalized ? std::sqrt((float)kN) : 1.0f;
-    fa.wvec = aligned(window, 8) ? 1 : 0;
-    const int64_t blocks = ceil_div(fa.frames_n, kTF);
-    MBRT_REQUIRE(blocks < kMaxGridX, MBRT_E_SHAPE, "%s: too many frames", op);
+    IstftBlockArgs ba{};
+    ba.spec = spec;
+    ba.w = window;
+    ba.part = static_cast<float*>(workspace);
+    ba.T = (uint32_t)frames;
+    ba.ntb = make_fastdiv((uint32_t)ntb);
+    ba.hop = make_fastdiv((uint32_t)hop);
+    ba.span = (uint32_t)((kTF - 1) * hop + kN);
+    ba.blocks = (uint32_t)(batch * ntb);
+    ba.wvec = aligned(window, 8) ? 1 : 0;
+    ba.spec_scale = normalized ? std::sqrt((float)kN) : 1.0f;
     if (spec_dtype == F32)
-        hipLaunchKernelGGL((istft_frames_kernel<kTF, F32>), dim3((unsigned)blocks), dim3(64 * kTF), 0, st, fa);
+        hipLaunchKernelGGL((istft_block_kernel<kTF, F32>), dim3(ba.blocks), dim3(64 * kTF), 0, st, ba);
     else
-        hipLaunchKernelGGL((istft_frames_kernel<kTF, BF16>), dim3((unsigned)blocks), dim3(64 * kTF), 0, st, fa);
+        hipLaunchKernelGGL((istft_block_kernel<kTF, BF16>), dim3(ba.blocks), dim3(64 * kTF), 0, st, ba);
     s = check_launch(op);
     if (s != MBRT_OK) return s;
-    MBRT_REQUIRE(batch * out_len < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: output of %lld samples is too large", op,
-                 (long long)(batch * out_len));
-    OlaArgs oa{};
-    oa.frames = fa.frames;
-    oa.w = window;
-    oa.out = out;
-    oa.out_len = make_fastdiv((uint32_t)out_len);
-    oa.total = (uint32_t)(batch * out_len);
-    const int64_t full = kN + (frames - 1) * hop;
-    oa.valid = (uint32_t)std::min<int64_t>(out_len, center ? full - kN : full);
-    oa.T = (uint32_t)frames;
-    oa.hop = make_fastdiv((uint32_t)hop);
-    oa.offset = center ? kN / 2 : 0;
-    hipLaunchKernelGGL(istft_ola_kernel, dim3((unsigned)grid_for(oa.total, 256)), dim3(256), 0, st, oa);
+    IstftFinalArgs fa{};
+    fa.part = ba.part;
+    fa.w = window;
+    fa.out = out;
+    fa.batch = (uint32_t)batch;
+    fa.out_len = (uint32_t)out_len;
+    fa.hop = make_fastdiv((uint32_t)hop);
+    fa.bhop = make_fastdiv((uint32_t)(kTF * hop));
+    fa.span = ba.span;
+    fa.ntb = (uint32_t)ntb;
+    fa.T = (uint32_t)frames;
+    fa.valid = (uint32_t)std::min<int64_t>(out_len, center ? full - kN : full);
+    fa.offset = center ? kN / 2 : 0;
+    hipLaunchKernelGGL(istft_final_kernel, dim3((unsigned)grid_for(out_len, 256)), dim3(256), 0, st, fa);
     return check_launch(op);
 }
 

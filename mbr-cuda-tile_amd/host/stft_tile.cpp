@@ -60,7 +60,8 @@ Tensor istft(const Tensor& complex_spec, int n_fft, int hop_length, int win_leng
     const int64_t n_out = mbrt_istft_output_length(T, hop_length, center ? 1 : 0, length);
     Tensor out = Tensor::empty({B, n_out}, DType::Float32);
     if (out.numel() == 0) return out;
-    const int64_t ws_bytes = mbrt_istft_workspace_bytes(B, T);
+    const int64_t ws_bytes = mbrt_istft_workspace_bytes(B, T, hop_length);
+    if (ws_bytes < 0) throw std::runtime_error("stft_tile::istft: hop_length out of range");
     Tensor frames = Tensor::empty({ws_bytes / 4}, DType::Float32);
     abi_check(mbrt_istft(spec.data_ptr(), (int)mbrt_code(spec.dtype()), win.data_f32(), out.data_f32(), B, F, T,
                          n_fft, hop_length, win_length, win.numel(), center ? 1 : 0, normalized ? 1 : 0, length,

@@ -360,6 +360,10 @@ def istft_output_length(frames: int, hop: int, center: bool = True, length: int 
     return int(_abi.lib().mbrt_istft_output_length(frames, hop, int(center), length))
 
 
+def istft_workspace_bytes(batch: int, frames: int, hop: int) -> int:
+    return int(_abi.lib().mbrt_istft_workspace_bytes(batch, frames, hop))
+
+
 def istft(spec: torch.Tensor, window: torch.Tensor, hop: int, center: bool = True, normalized: bool = False,
           length: int = -1, out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
           n_fft: int = N_FFT, win_length: int = N_FFT, stream=None) -> torch.Tensor:
@@ -370,7 +374,7 @@ def istft(spec: torch.Tensor, window: torch.Tensor, hop: int, center: bool = Tru
     if out is None:
         out = torch.empty((B, max(n_out, 0)), dtype=torch.float32, device=spec.device)
     _contig(out)
-    need = int(_abi.lib().mbrt_istft_workspace_bytes(B, T))
+    need = int(_abi.lib().mbrt_istft_workspace_bytes(B, T, hop))
     if workspace is None:
         workspace = torch.empty(max(need, 0) // 4, dtype=torch.float32, device=spec.device)
     _abi.call("mbrt_istft", _p(spec), dtype_code(spec), _p(window), _p(out), B, F, T, n_fft, hop, win_length,

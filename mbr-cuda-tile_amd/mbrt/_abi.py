@@ -100,7 +100,7 @@ SIGNATURES: dict[str, list] = {
     "mbrt_stft_num_frames": [L, L, I],
     "mbrt_stft": [P, P, P, L, L, L, L, L, L, I, I, P],
     "mbrt_istft_output_length": [L, L, I, L],
-    "mbrt_istft_workspace_bytes": [L, L],
+    "mbrt_istft_workspace_bytes": [L, L, L],
     "mbrt_istft": [P, I, P, P, L, L, L, L, L, L, L, I, I, L, P, L, P],
     "mbrt_chunk_accumulate": [P, P, P, P, L, L, L, L, P],
     "mbrt_chunk_normalize": [P, P, L, L, P],
