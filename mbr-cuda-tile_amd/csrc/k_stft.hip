@@ -18,12 +18,13 @@
 //
 // STFT   one kernel: reflect-padded frame load with the window applied, FFT, real split,
 //        optional 1/sqrt(2048), transposed store.
-// iSTFT  two kernels: (1) transposed spectrum load (f32 or bf16, times sqrt(2048) when
-//        normalized), inverse split, inverse FFT, window and 1/2048, frames to a caller
-//        workspace [B*T, 2048]; (2) overlap-add as a gather: each output sample sums the
-//        <= ceil(2048/hop) frames that cover it in frame order and divides by the window
-//        sum of squares where that exceeds 1e-8; centre trim and the `length` trim / zero
-//        fill are part of the same pass.  No atomics: the result is deterministic.
+// iSTFT  two kernels: (1) per block of kTF frames of one signal: transposed spectrum load
+//        (f32 or bf16, times sqrt(2048) when normalized), inverse split, inverse FFT,
+//        window and 1/2048 into the frame's LDS slot, then the block's frames overlap-added
+//        in LDS (frame order) into a partial signal in a caller workspace; (2) per output
+//        sample: the partials of the blocks covering it (block order), divided by the
+//        window sum of squares where that exceeds 1e-8; centre trim and the `length` trim /
+//        zero fill are part of the same pass.  No atomics: the result is deterministic.
 #include "abi_common.hpp"
 
 #include <cmath>
