@@ -9,9 +9,11 @@
 // B[8(l/16)+j][l%16], C[4(l/16)+i][l%16]):
 //   S^T = K Q^T     8 MFMAs: A = K rows from LDS, B = the wave's Q fragment (registers).
 //                   Lane l then holds S^T[key 16kb + 4(l/16) + i][query l%16].
-//   online softmax  per query l%16: max/sum over the lane's 16 keys, then over the four
-//                   lane groups (xor 16, xor 32); the accumulator is rescaled in place
-//                   only when the max outgrows the exponent reference by 2^8.
+//   online softmax  per query l%16: each lane keeps a partial row sum over its own keys
+//                   (the four lane groups are added after the last tile).  The exponent
+//                   reference moves only when a score outgrows it by 2^8; only then is
+//                   the max taken over the four lane groups (xor 16, xor 32) and the
+//                   accumulator rescaled in place.
 //   O^T += V^T P^T  16 MFMAs: B = P^T straight from the S^T registers, as a bf16 pair
 //                   P_hi + P_lo; A = V^T read from the row-major V tile with the gfx950
 //                   LDS transpose read (ds_read_b64_tr_b16).
@@ -79,9 +81,12 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
     const int tid = threadIdx.x;
     const int lane = tid % 64, g = lane / 16, c = lane % 16;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
-    // one linear grid, query tiles of one (b, h) adjacent so that they share its K/V in L2
-    const int64_t bh = blockIdx.x / a.qtiles;
-    const int q0 = (blockIdx.x % a.qtiles) * kQB + w * kQWave * QS;
+    // one linear grid of (b, h, query tile), the query tiles of one (b, h) adjacent; each
+    // XCD walks one contiguous range of it, so that the query tiles of a (b, h) run on one
+    // XCD, close in time, and read its K/V once into that XCD's L2
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int64_t bh = tile / a.qtiles;
+    const int q0 = (tile % a.qtiles) * kQB + w * kQWave * QS;
     const __bf16* kbase = a.k + bh * a.nk * kHeadDim;
     const __bf16* vbase = a.v + bh * a.nk * kHeadDim;
 
@@ -157,36 +162,37 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
         }
 #pragma unroll
         for (int x = 0; x < QS; ++x) {
-            // m[x] is the exponent reference in log2 units.  It moves only when the tile's
-            // scaled max exceeds it by more than kLazy: P <= 2^kLazy then, harmless in f32
-            // and in the bf16 pair, and the accumulator is rescaled about once per query.
+            // m[x] is the exponent reference in log2 units, the same in the four lanes of a
+            // query.  It moves only when a score exceeds it by more than kLazy (scaled):
+            // P <= 2^kLazy otherwise, harmless in f32 and in the bf16 pair, and the
+            // accumulator is rescaled about once per query.  The lane's own 16 scores decide
+            // whether to look; the max over the query's four lanes is formed only then.
             float mx = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb)
                 mx = fmaxf(mx, fmaxf(fmaxf(st[x][kb][0], st[x][kb][1]), fmaxf(st[x][kb][2], st[x][kb][3])));
-            mx = xor_max(mx) * a.scale_log2e;
-            // wave-uniform branch: the rescale runs only on the (rare) tiles where some query
-            // of the wave outgrows its reference; queries that do not keep alpha = 1
-            const bool grow = mx > m[x] + kLazy;
-            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-                const float mn = grow ? mx : m[x];
+            // wave-uniform branch, taken on the (rare) tiles where some score of the wave
+            // outgrows its reference; queries that do not grow keep alpha = 1
+            if (__builtin_amdgcn_ballot_w64(mx * a.scale_log2e > m[x] + kLazy) != 0) {
+                mx = xor_max(mx) * a.scale_log2e;
+                const float mn = mx > m[x] + kLazy ? mx : m[x];
                 const float alpha = __builtin_amdgcn_exp2f(m[x] - mn);
                 l[x] *= alpha;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) o[x][db] *= alpha;
                 m[x] = mn;
             }
-            float psum = 0.0f;
+            // l[x] is the lane's partial row sum over its own keys; the four lanes of a
+            // query are added once, after the last tile
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float p = __builtin_amdgcn_exp2f(fmaf(st[x][kb][i], a.scale_log2e, -m[x]));
                     st[x][kb][i] = p;
-                    psum += p;
+                    l[x] += p;
                 }
             }
-            l[x] += xor_sum(psum);
         }
 
         // O^T += V^T P^T over the two 32-key chunks.  P = P_hi + P_lo, both bf16: hi is P
@@ -233,9 +239,10 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
 
 #pragma unroll
     for (int x = 0; x < QS; ++x) {
+        const float lsum = xor_sum(l[x]);
         const int q = q0 + 16 * x + c;
         if (q >= a.nq) continue;
-        const float inv = 1.0f / l[x];
+        const float inv = 1.0f / lsum;
         const int64_t obase = (bh * a.nq + q) * kHeadDim;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
