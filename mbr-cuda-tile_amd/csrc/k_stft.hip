@@ -11,13 +11,15 @@
 // both the strided and the contiguous access patterns free of bank conflicts).  The STFT
 // takes the last pass's butterflies in mirror pairs so the real split needs no exchange.
 //
-// Workgroup = kTF waves = kTF consecutive frames (flattened over batch x time).  The
-// frames' spectra stay in LDS so that the [B, F, T] layout is written (STFT) or read
-// (iSTFT) as runs of kTF consecutive frames per bin, instead of one 8-byte element per
-// 8*T bytes.
+// Workgroup = kTF waves = kTF consecutive frames of one signal.  The frames' spectra stay
+// in LDS so that the [B, F, T] layout is written (STFT) or read (iSTFT) as runs of kTF
+// consecutive frames per bin, instead of one 8-byte element per 8*T bytes.
 //
-// STFT   one kernel: reflect-padded frame load with the window applied, FFT, real split,
-//        optional 1/sqrt(2048), transposed store.
+// STFT   one kernel: the workgroup's sample span ((kTF - 1) hop + 2048 samples, reflect
+//        padded at the signal ends) and the window are staged once into the frame slots
+//        with coalesced loads (for hops up to 1910; larger hops read frame by frame), each
+//        wave takes its windowed frame from there, then FFT, real split, optional
+//        1/sqrt(2048), transposed store.
 // iSTFT  two kernels: (1) per block of kTF frames of one signal: transposed spectrum load
 //        (f32 or bf16, times sqrt(2048) when normalized), inverse split, inverse FFT,
 //        window and 1/2048 into the frame's LDS slot, then the block's frames overlap-added
@@ -272,11 +274,13 @@ struct StftArgs {
     const float* w;    // [2048]
     float2* out;       // [B, 1025, T] complex
     int L;
-    uint32_t frames;   // B * T
-    FastDiv T;         // frame index -> (signal, frame in signal)
+    uint32_t T;        // frames per signal
+    FastDiv ntb;       // workgroups per signal: block index -> (signal, block in signal)
     int hop;
     int offset;        // 1024 when centred (reflect padding), else 0
     int wvec;          // window is 8-byte aligned: read it as float2
+    int xvec;          // signal is 16-byte aligned: stage it with float4 loads
+    int staged;        // the workgroup's sample span and the window fit its frame slots
     float norm;
 };
 
@@ -326,23 +330,87 @@ __device__ __forceinline__ void load_frame(const StftArgs& a, uint32_t b, uint32
     }
 }
 
+// Stages the workgroup's window (2048 floats) and sample span ((nf - 1) hop + 2048 floats
+// from sample s of signal b) into LDS: the span with aligned float4 loads when it lies
+// inside the signal, else sample by sample through the reflect-then-clamp rule.  Returns
+// the span's offset in the staging area.
+template <int NT>
+__device__ __forceinline__ int stage_span(const StftArgs& a, float* stage, uint32_t b, int s, int span) {
+    const int tid = threadIdx.x;
+    if (a.wvec) {
+        for (int i = tid; i < kN / 2; i += NT)
+            reinterpret_cast<float2*>(stage)[i] = reinterpret_cast<const float2*>(a.w)[i];
+    } else {
+        for (int i = tid; i < kN; i += NT) stage[i] = a.w[i];
+    }
+    float* xst = stage + kN;
+    if (a.xvec && s >= 0 && s + span <= a.L) {
+        const int64_t base = (int64_t)b * a.L + s, end = base + span;
+        const int64_t a4 = base & ~int64_t(3);  // >= 0; float4 loads from a4 are 16-byte aligned
+        const int xoff = (int)(base - a4), n4 = (xoff + span + 3) >> 2;
+        for (int i = tid; i < n4; i += NT) {
+            const int64_t e = a4 + 4 * (int64_t)i;
+            float4 v;
+            if (e + 4 <= end) {
+                v = *reinterpret_cast<const float4*>(a.x + e);
+            } else {  // the last partial vector: nothing at or past the span's end is read
+                v.x = e < end ? a.x[e] : 0.0f;
+                v.y = e + 1 < end ? a.x[e + 1] : 0.0f;
+                v.z = e + 2 < end ? a.x[e + 2] : 0.0f;
+                v.w = 0.0f;
+            }
+            reinterpret_cast<float4*>(xst)[i] = v;
+        }
+        return xoff;
+    }
+    const float* xb = a.x + (int64_t)b * a.L;
+    for (int j = tid; j < span; j += NT) {
+        // reflect once about the ends, then clamp (the reference's pad_reflect rule)
+        int c = s + j;
+        if (c < 0) c = -c;
+        if (c >= a.L) c = 2 * (a.L - 1) - c;
+        c = c < 0 ? 0 : (c > a.L - 1 ? a.L - 1 : c);
+        xst[j] = xb[c];
+    }
+    return 0;
+}
+
 template <int TF>
 __global__ __launch_bounds__(64 * TF) void stft_kernel(StftArgs a) {
     constexpr int NT = 64 * TF;
     __shared__ __attribute__((aligned(16))) float2 lds[TF * kSlot + kTwSlots];
     float2* tw = lds + TF * kSlot;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const uint32_t g0 = xcd_runs<kXcdRun>(blockIdx.x, gridDim.x) * TF;
-    const uint32_t g = g0 + wave;  // this wave's frame
-    const bool live = g < a.frames;
+    // workgroup = frames t0 .. t0 + nf - 1 of signal b
+    uint32_t b, tb;
+    fdivmod(xcd_runs<kXcdRun>(blockIdx.x, gridDim.x), a.ntb, b, tb);
+    const uint32_t t0 = tb * TF;
+    const int nf = (int)min((uint32_t)TF, a.T - t0);
+    const bool live = wave < nf;
     cf v[16];
-    if (live) {
-        uint32_t b, t;
-        fdivmod(g, a.T, b, t);
-        load_frame(a, b, t, lane, v);
+    if (a.staged) {
+        // the frames of a workgroup overlap (hop < 2048): their span and the window are read
+        // from HBM once, coalesced, into the frame slots, and each wave takes its frame there
+        const int s = (int)t0 * a.hop - a.offset;
+        float* stage = reinterpret_cast<float*>(lds);
+        const int xoff = stage_span<NT>(a, stage, b, s, (nf - 1) * a.hop + kN);
+        load_twiddles<NT>(tw);
+        __syncthreads();
+        if (live) {
+            const float* xs = stage + kN + xoff + wave * a.hop;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int n = 2 * (lane + 64 * q);
+                const float2 w = reinterpret_cast<const float2*>(stage)[lane + 64 * q];
+                v[q] = cf{xs[n] * w.x, xs[n + 1] * w.y};
+            }
+        }
+        __syncthreads();  // the staging area becomes the frame slots
+    } else {
+        if (live) load_frame(a, b, t0 + wave, lane, v);
+        load_twiddles<NT>(tw);
+        __syncthreads();
     }
-    load_twiddles<NT>(tw);
-    __syncthreads();
     if (live) {
         float2* slot = lds + wave * kSlot;
         fft_pass12<false>(v, slot, tw, lane);
@@ -372,16 +440,13 @@ __global__ __launch_bounds__(64 * TF) void stft_kernel(StftArgs a) {
         }
     }
     __syncthreads();
-    // transposed store: thread -> (frame tl, bins fr, fr + 64, ...)
+    // transposed store: thread -> (frame t0 + tl, bins fr, fr + 64, ...)
     const int tl = threadIdx.x % TF, fr = threadIdx.x / TF;
-    const uint32_t gs = g0 + tl;
-    if (gs >= a.frames) return;
-    uint32_t bs, ts;
-    fdivmod(gs, a.T, bs, ts);
-    float2* dst = a.out + ((int64_t)bs * kBins * a.T.d + ts);
+    if (tl >= nf) return;
+    float2* dst = a.out + ((int64_t)b * kBins * a.T + t0 + tl);
     const float2* src = lds + tl * kSlot;
-    const int64_t step = (int64_t)(NT / TF) * a.T.d;
-    dst += (int64_t)fr * a.T.d;
+    const int64_t step = (int64_t)(NT / TF) * a.T;
+    dst += (int64_t)fr * a.T;
 #pragma unroll 4
     for (int f = fr; f < kBins; f += NT / TF, dst += step) {
         const float2 X = src[pad16(f)];
@@ -617,13 +682,17 @@ int mbrt_stft(const float* signal, const float* window, float* out, int64_t batc
     a.w = window;
     a.out = reinterpret_cast<float2*>(out);
     a.L = (int)length;
-    a.frames = (uint32_t)(batch * T);
-    a.T = make_fastdiv((uint32_t)T);
+    a.T = (uint32_t)T;
+    const int64_t ntb = ceil_div(T, kTF);
+    a.ntb = make_fastdiv((uint32_t)ntb);
     a.hop = (int)hop;
     a.offset = center ? kN / 2 : 0;
     a.norm = normalized ? 1.0f / std::sqrt((float)kN) : 1.0f;
     a.wvec = aligned(window, 8) ? 1 : 0;
-    const int64_t blocks = ceil_div(a.frames, kTF);
+    a.xvec = aligned(signal, 16) ? 1 : 0;
+    // window + span (+ up to 6 floats of float4 alignment) within the kTF frame slots
+    a.staged = kN + (kTF - 1) * hop + kN + 6 <= 2 * kTF * kSlot ? 1 : 0;
+    const int64_t blocks = batch * ntb;
     MBRT_REQUIRE(blocks < kMaxGridX, MBRT_E_SHAPE, "%s: too many frames", op);
     hipLaunchKernelGGL((stft_kernel<kTF>), dim3((unsigned)blocks), dim3(64 * kTF), 0, as_stream(stream), a);
     return check_launch(op);

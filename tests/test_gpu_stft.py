@@ -42,6 +42,9 @@ def test_hann_window(orc, dev, size):
     (1, 700, 441, True, False, "hann"),      # shorter than the pad: reflect, then clamp
     (1, 5000, 7, True, False, "rand"),       # small hop: 715 frames
     (2, 10000, 3000, False, True, "hann"),   # hop > n_fft
+    (3, 9001, 441, True, False, "rand"),     # signal rows start at every 4-byte alignment
+    (2, 20000, 1910, True, False, "hann"),   # largest hop whose 8-frame span is staged in LDS
+    (2, 20000, 1911, True, False, "hann"),   # smallest hop read frame by frame
 ])
 def test_stft_shapes(orc, dev, B, L, hop, center, normalized, win):
     say(f"stft B={B} L={L} hop={hop} center={center} normalized={normalized} window={win}")
@@ -52,6 +55,24 @@ def test_stft_shapes(orc, dev, B, L, hop, center, normalized, win):
     ref = orc.stft(x, w, hop, center, normalized)
     den = orc.stft_den(x, w, hop, center, normalized)
     print("stft errors", assert_close(to_host(out, F32), ref, F32, "stft", den=den))
+
+
+@pytest.mark.parametrize("shift", [1, 2, 3])
+def test_stft_unaligned_buffers(orc, dev, shift):
+    """Signal and window that start off a 16-byte (window: 8-byte) boundary."""
+    say(f"stft unaligned by {shift} floats")
+    B, L, hop = 2, 6000, 441
+    x = orc.randn((B, L), seed=0x4D425200B2, stream=shift)
+    w = _window(orc, "rand")
+    xbuf = torch.zeros(B * L + shift, device=dev)
+    xbuf[shift:] = to_dev(x, F32).reshape(-1)
+    wbuf = torch.zeros(2048 + shift, device=dev)
+    wbuf[shift:] = to_dev(w, F32)
+    out = mbrt.stft(xbuf[shift:].view(B, L), wbuf[shift:], hop, True, False)
+    torch.cuda.synchronize()
+    ref = orc.stft(x, w, hop, True, False)
+    den = orc.stft_den(x, w, hop, True, False)
+    print("stft unaligned errors", assert_close(to_host(out, F32), ref, F32, "stft unaligned", den=den))
 
 
 def test_stft_full_shape(orc, dev):
