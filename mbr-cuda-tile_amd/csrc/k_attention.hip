@@ -2,7 +2,9 @@
 // the time attention (N = 801) and frequency attention (N = 60) of the band-split
 // transformer (src/mbr_cuda_tile.cu:6530-6709, src/mbr_time_attention_cutile.cu:108-196).
 // The [BH, N, N] score matrix never reaches HBM: each workgroup streams K/V tiles through
-// LDS and keeps an online softmax (running max m, running sum l) per query.
+// LDS and keeps an online softmax (running max m, running sum l) per query.  The tiles go
+// from HBM straight into LDS (global_load_lds_dwordx4), double buffered: the next tile
+// loads while the current one is computed, one barrier per tile.
 //
 // Workgroup = 4 waves of one (b, h); wave w owns 16 or 32 queries (QS sub-blocks of 16).
 // Per 64-key tile, with v_mfma_f32_16x16x32_bf16 (lane l: A[l%16][8(l/16)+j],
@@ -39,10 +41,6 @@ constexpr int kQWave = 16;     // queries per wave
 constexpr int kWaves = 4;
 constexpr int kQBlock = kQWave * kWaves;
 constexpr float kLazy = 8.0f;  // log2 units the running max may outgrow the exponent reference
-#ifndef MBRT_ATTN_PAD
-#define MBRT_ATTN_PAD 8
-#endif
-constexpr int kPad = MBRT_ATTN_PAD;  // LDS row padding (bf16 elements)
 #ifndef MBRT_ATTN_QS2_MIN
 #define MBRT_ATTN_QS2_MIN 1  // 32 queries per wave when n_q exceeds this many 64-query blocks
 #endif
@@ -51,6 +49,15 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;  // an LDS-resident bf16x4
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void global_void;
+
+// K/V tiles in LDS: [64 keys][64 d] bf16 without padding, a key row = eight 16-byte chunks.
+// Logical chunk j of key r sits at chunk j ^ (r & 7), so that the 16-byte fragment reads
+// of 8 consecutive keys (same logical chunk) fall on 8 different bank groups.
+__device__ __forceinline__ int tile_at(int r, int chunk, int within) {
+    return r * kHeadDim + 8 * (chunk ^ (r & 7)) + within;
+}
 
 struct AttnArgs {
     const __bf16* q;
@@ -75,8 +82,12 @@ __device__ __forceinline__ float xor_sum(float x) {
 // feeds QS MFMAs, so longer sequences use QS = 2 (128 queries per workgroup).
 template <int ODT, int QS>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) __bf16 ks[kKeys][kHeadDim + kPad];   // K tile [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 vs[kKeys][kHeadDim + kPad];   // V tile [key][d]
+    // two K and two V tiles: the next pair is loaded (straight into LDS) while the current
+    // one is read
+    __shared__ __attribute__((aligned(16))) __bf16 k0[kKeys * kHeadDim];
+    __shared__ __attribute__((aligned(16))) __bf16 v0[kKeys * kHeadDim];
+    __shared__ __attribute__((aligned(16))) __bf16 k1[kKeys * kHeadDim];
+    __shared__ __attribute__((aligned(16))) __bf16 v1[kKeys * kHeadDim];
     constexpr int kQB = kQWave * QS * kWaves;  // queries per workgroup
     const int tid = threadIdx.x;
     const int lane = tid % 64, g = lane / 16, c = lane % 16;
@@ -109,31 +120,33 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
         l[x] = 0.0f;
     }
 
-    // K/V tiles: 64 keys x 64 d = 512 16-byte vectors each, 2 per thread.  The next tile
-    // is fetched into registers while the current one is computed from LDS.
-    // Thread t stages the 16-byte vectors t and t + 256 (key = vector / 8) of each tile.
-    bf16x8 kv[2], vv[2];
-    // element offsets within one (b, h) fit 32 bits (n_k * 64 < 2^31 is checked on the host)
-    auto fetch = [&](int kt) {
+    // Tile loads go from HBM straight into LDS (global_load_lds_dwordx4: lane i of a wave
+    // instruction writes the 16 bytes at base + 16 i).  Wave w loads keys 16w .. 16w + 15 of
+    // a tile, 8 per instruction: lane i -> key 16w + 8u + i/8, stored chunk i % 8, which
+    // holds logical chunk (i % 8) ^ (i / 8).  Keys past N load a clamped row (masked later).
+    // Element offsets within one (b, h) fit 32 bits (n_k * 64 < 2^31 is checked on the host).
+    auto load_tile = [&](int kt, int buf) {
+        __bf16* kd = buf ? k1 : k0;
+        __bf16* vd = buf ? v1 : v0;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int vec = tid + 256 * u, dc = (vec & 7) * 8;
-            const uint32_t off = (uint32_t)min(kt + (vec >> 3), a.nk - 1) * kHeadDim + dc;
-            kv[u] = *reinterpret_cast<const bf16x8*>(kbase + off);
-            vv[u] = *reinterpret_cast<const bf16x8*>(vbase + off);
+            const int r0 = 16 * w + 8 * u, key = r0 + (lane >> 3);
+            const uint32_t off = (uint32_t)min(kt + key, a.nk - 1) * kHeadDim + 8 * ((lane & 7) ^ (lane >> 3));
+            __builtin_amdgcn_global_load_lds((global_void*)(kbase + off), (lds_void*)&kd[r0 * kHeadDim], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(vbase + off), (lds_void*)&vd[r0 * kHeadDim], 16, 0, 0);
         }
     };
-    fetch(0);
-    for (int kt = 0; kt < a.nk; kt += kKeys) {
-        __syncthreads();  // the previous tile is no longer read
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int vec = tid + 256 * u, key = vec >> 3, dc = (vec & 7) * 8;
-            *reinterpret_cast<bf16x8*>(&ks[key][dc]) = kv[u];
-            *reinterpret_cast<bf16x8*>(&vs[key][dc]) = vv[u];
-        }
+    load_tile(0, 0);
+    // One key tile: ks/vs hold it, kn/vn receive the next one.  The two buffer pairs are
+    // separate LDS objects and the loop below is unrolled by two, so the compiler sees that
+    // the loads in flight into kn/vn never alias the reads of ks/vs and waits for them only
+    // at the next tile's barrier.
+    auto tile_step = [&](int kt, const __bf16* ks, const __bf16* vs, int nbuf) {
+        // this wave's loads of the tile have landed (vmcnt 0); after the barrier every
+        // wave's have, and no wave still reads the other buffer, which is refilled next
+        __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
-        if (kt + kKeys < a.nk) fetch(kt + kKeys);
+        if (kt + kKeys < a.nk) load_tile(kt + kKeys, nbuf);
 
         // S^T = K Q^T for the 4 key blocks of the tile and every query sub-block
         f32x4 st[QS][4];
@@ -143,7 +156,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
             for (int x = 0; x < QS; ++x) st[x][kb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&ks[16 * kb + c][32 * s + 8 * g]);
+                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&ks[tile_at(16 * kb + c, 4 * s + g, 0)]);
 #pragma unroll
                 for (int x = 0; x < QS; ++x)
                     st[x][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[x][s], st[x][kb], 0, 0, 0);
@@ -224,9 +237,9 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
                 // element i%4 of the 8-byte chunks of lanes 4r + i/4 (r = 0..3), so lane
                 // (g, c) supplies V[32cc + 4g + c/4 (+16)][16db + 4(c%4) ..] and receives
                 // V[32cc + 4g + r (+16)][16db + c] for r = 0..3: slots j and 4 + j.
-                const int vrow = 32 * cc + 4 * g + (c >> 2), vcol = 16 * db + 4 * (c & 3);
-                const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(&vs[vrow][vcol]));
-                const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(&vs[vrow + 16][vcol]));
+                const int vrow = 32 * cc + 4 * g + (c >> 2), vch = 2 * db + ((c & 3) >> 1), vin = 4 * (c & 1);
+                const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(&vs[tile_at(vrow, vch, vin)]));
+                const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(&vs[tile_at(vrow + 16, vch, vin)]));
                 const bf16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
                 for (int x = 0; x < QS; ++x) {
@@ -235,6 +248,10 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
                 }
             }
         }
+    };
+    for (int kt = 0; kt < a.nk; kt += 2 * kKeys) {
+        tile_step(kt, k0, v0, 1);
+        if (kt + kKeys < a.nk) tile_step(kt + kKeys, k1, v1, 0);
     }
 
 #pragma unroll
