@@ -132,8 +132,14 @@ __device__ __forceinline__ cf twiddle(const float2* tw, int i) {
 // Copies W^i, i < 1024, into the workgroup's LDS table (all threads take part).
 template <int NT>
 __device__ __forceinline__ void load_twiddles(float2* tw) {
+    static_assert(kTwHalf % NT == 0, "threads per workgroup divide the table");
+    constexpr int kPer = kTwHalf / NT;
     const float2* src = reinterpret_cast<const float2*>(kTwiddles.v);
-    for (int i = threadIdx.x; i < kTwHalf; i += NT) tw[tw_pos(i)] = src[i];
+    float2 t[kPer];  // every load in flight before the first LDS write
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) t[k] = src[threadIdx.x + k * NT];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) tw[tw_pos(threadIdx.x + k * NT)] = t[k];
 }
 
 template <bool INV>
@@ -336,41 +342,68 @@ __device__ __forceinline__ void load_frame(const StftArgs& a, uint32_t b, uint32
 // the span's offset in the staging area.
 template <int NT>
 __device__ __forceinline__ int stage_span(const StftArgs& a, float* stage, uint32_t b, int s, int span) {
+    // Loads are issued in groups of 4 per thread before their LDS writes, so that each
+    // thread has several in flight.
     const int tid = threadIdx.x;
     if (a.wvec) {
-        for (int i = tid; i < kN / 2; i += NT)
-            reinterpret_cast<float2*>(stage)[i] = reinterpret_cast<const float2*>(a.w)[i];
+        static_assert((kN / 2) % NT == 0, "threads per workgroup divide the window");
+        constexpr int kPer = kN / 2 / NT;
+        float2 wv[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) wv[k] = reinterpret_cast<const float2*>(a.w)[tid + k * NT];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) reinterpret_cast<float2*>(stage)[tid + k * NT] = wv[k];
     } else {
-        for (int i = tid; i < kN; i += NT) stage[i] = a.w[i];
+        constexpr int kPer = kN / NT;
+        float wv[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) wv[k] = a.w[tid + k * NT];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) stage[tid + k * NT] = wv[k];
     }
     float* xst = stage + kN;
     if (a.xvec && s >= 0 && s + span <= a.L) {
         const int64_t base = (int64_t)b * a.L + s, end = base + span;
         const int64_t a4 = base & ~int64_t(3);  // >= 0; float4 loads from a4 are 16-byte aligned
         const int xoff = (int)(base - a4), n4 = (xoff + span + 3) >> 2;
-        for (int i = tid; i < n4; i += NT) {
-            const int64_t e = a4 + 4 * (int64_t)i;
-            float4 v;
-            if (e + 4 <= end) {
-                v = *reinterpret_cast<const float4*>(a.x + e);
-            } else {  // the last partial vector: nothing at or past the span's end is read
-                v.x = e < end ? a.x[e] : 0.0f;
-                v.y = e + 1 < end ? a.x[e + 1] : 0.0f;
-                v.z = e + 2 < end ? a.x[e + 2] : 0.0f;
-                v.w = 0.0f;
+        for (int i0 = tid; i0 < n4; i0 += 4 * NT) {
+            float4 v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int i = i0 + k * NT;
+                const int64_t e = a4 + 4 * (int64_t)i;
+                if (i >= n4) {
+                    v[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                } else if (e + 4 <= end) {
+                    v[k] = *reinterpret_cast<const float4*>(a.x + e);
+                } else {  // the last partial vector: nothing at or past the span's end is read
+                    v[k].x = e < end ? a.x[e] : 0.0f;
+                    v[k].y = e + 1 < end ? a.x[e + 1] : 0.0f;
+                    v[k].z = e + 2 < end ? a.x[e + 2] : 0.0f;
+                    v[k].w = 0.0f;
+                }
             }
-            reinterpret_cast<float4*>(xst)[i] = v;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (i0 + k * NT < n4) reinterpret_cast<float4*>(xst)[i0 + k * NT] = v[k];
         }
         return xoff;
     }
     const float* xb = a.x + (int64_t)b * a.L;
-    for (int j = tid; j < span; j += NT) {
-        // reflect once about the ends, then clamp (the reference's pad_reflect rule)
-        int c = s + j;
-        if (c < 0) c = -c;
-        if (c >= a.L) c = 2 * (a.L - 1) - c;
-        c = c < 0 ? 0 : (c > a.L - 1 ? a.L - 1 : c);
-        xst[j] = xb[c];
+    for (int j0 = tid; j0 < span; j0 += 4 * NT) {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            // reflect once about the ends, then clamp (the reference's pad_reflect rule)
+            int c = s + j0 + k * NT;
+            if (c < 0) c = -c;
+            if (c >= a.L) c = 2 * (a.L - 1) - c;
+            c = c < 0 ? 0 : (c > a.L - 1 ? a.L - 1 : c);
+            v[k] = j0 + k * NT < span ? xb[c] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (j0 + k * NT < span) xst[j0 + k * NT] = v[k];
     }
     return 0;
 }
@@ -495,17 +528,22 @@ __global__ __launch_bounds__(64 * TF) void istft_block_kernel(IstftBlockArgs a) 
     const uint32_t t0 = tb * TF;
     const uint32_t nf = min((uint32_t)TF, a.T - t0);
     {
-        // transposed spectrum load: thread -> (frame tl, bins fr, fr + 64, ...)
+        // transposed spectrum load: thread -> (frame tl, bins fr + 64 k, k = 0..15, and bin
+        // 1024 for fr = 0); all 16 (17) loads are in flight before the first LDS write
+        static_assert(NT / TF == 64, "64 bin rows per pass");
         const int tl = threadIdx.x % TF, fr = threadIdx.x / TF;
         if ((uint32_t)tl < nf) {
-            int64_t idx = (int64_t)b * kBins * a.T + t0 + tl + (int64_t)fr * a.T;
-            const int64_t step = (int64_t)(NT / TF) * a.T;
+            const int64_t idx = (int64_t)b * kBins * a.T + t0 + tl + (int64_t)fr * a.T;
+            const int64_t step = (int64_t)64 * a.T;
+            float2 X[17];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) X[k] = load_bin<SDT>(a.spec, idx + k * step);
+            if (fr == 0) X[16] = load_bin<SDT>(a.spec, idx + 16 * step);
             float2* slot = lds + tl * kSlot;
-#pragma unroll 4
-            for (int f = fr; f < kBins; f += NT / TF, idx += step) {
-                const float2 X = load_bin<SDT>(a.spec, idx);
-                slot[pad16(f)] = make_float2(X.x * a.spec_scale, X.y * a.spec_scale);
-            }
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                slot[pad16(fr + 64 * k)] = make_float2(X[k].x * a.spec_scale, X[k].y * a.spec_scale);
+            if (fr == 0) slot[pad16(kN / 2)] = make_float2(X[16].x * a.spec_scale, X[16].y * a.spec_scale);
         }
     }
     load_twiddles<NT>(tw);
