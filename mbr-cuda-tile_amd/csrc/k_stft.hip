@@ -625,20 +625,55 @@ __global__ __launch_bounds__(256) void istft_final_kernel(IstftFinalArgs a) {
             continue;
         }
         const uint32_t s = so + a.offset;
-        // window sum of squares in frame order (f32), as the reference's window_sum
+        // window sum of squares in frame order (f32), as the reference's window_sum; the
+        // loads go 8 at a time, all in flight before their terms are added
         const uint32_t thi = min(a.T - 1, fdiv(s, a.hop));
         const uint32_t tlo = s >= (uint32_t)kN ? fdiv(s - kN, a.hop) + 1 : 0;
         float ws = 0.0f;
-        uint32_t n = s - tlo * hop;
-        for (uint32_t t = tlo; t <= thi; ++t, n -= hop) {
+        for (uint32_t t = tlo; t <= thi; t += 8) {
+            float wv[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) wv[k] = a.w[t + k <= thi ? s - (t + k) * hop : 0];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) {
 #pragma clang fp contract(off)
-            const float wn = a.w[n];
-            ws = ws + wn * wn;
+                if (t + k <= thi) ws = ws + wv[k] * wv[k];
+            }
         }
         // blocks covering s, in block order; a block's partial is shorter when it is the last
         // one of its signal
         const uint32_t bhi = min(a.ntb - 1, fdiv(s, a.bhop));
         const uint32_t blo = s >= a.span ? fdiv(s - a.span, a.bhop) + 1 : 0;
+        if (bhi <= blo + 1) {
+            // at most two blocks (every hop >= 256): the same two offsets for every signal,
+            // whose loads go 4 signals at a time
+            bool v[2];
+            int64_t off[2];
+#pragma unroll
+            for (uint32_t i = 0; i < 2; ++i) {
+                const uint32_t tb = blo + i, u = s - tb * bhop;
+                v[i] = tb <= bhi && u < (min((uint32_t)kTF, a.T - tb * kTF) - 1) * hop + kN;
+                off[i] = v[i] ? (int64_t)tb * a.span + u : 0;
+            }
+            for (uint32_t b0 = 0; b0 < a.batch; b0 += 4) {
+                float p[4][2];
+#pragma unroll
+                for (uint32_t k = 0; k < 4; ++k) {
+                    const float* pb = a.part + (int64_t)min(b0 + k, a.batch - 1) * a.ntb * a.span;
+                    p[k][0] = pb[off[0]];
+                    p[k][1] = pb[off[1]];
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < 4; ++k) {
+                    if (b0 + k >= a.batch) break;
+                    float acc = 0.0f;
+                    if (v[0]) acc += p[k][0];
+                    if (v[1]) acc += p[k][1];
+                    a.out[(int64_t)(b0 + k) * a.out_len + so] = ws > 1.0e-8f ? acc / ws : acc;
+                }
+            }
+            continue;
+        }
 #pragma unroll 4
         for (uint32_t b = 0; b < a.batch; ++b) {
             const float* pb = a.part + (int64_t)b * a.ntb * a.span;
