@@ -10,11 +10,12 @@ shape (BL-1 .. BL-5), each on synthetic inputs already resident in HBM:
         permute bf16 [4, 801, 60, 384] -> [4, 60, 801, 384] and back
   BL-5  band gather and mask merge, batch 4, 60 mel bands (3958 stereo band-bins)
 value = sum of algorithmic bytes / sum of op times (GB/s, all ops); per-op GB/s and the
-fraction of the 8 TB/s HBM peak are in config.per_op.  Op times are HIP events recorded
-on the stream the kernels run on.  The K steps are timed op-major: each op's K calls run
-back to back, so every op pays for its own cache write-backs.  Each op cycles through enough buffer sets that the
-working set between two uses of a set exceeds 1 GB, so the 256 MB MALL cannot serve
-repeats.  Algorithmic bytes count every input read once and every output written once.
+fraction of the 8 TB/s HBM peak are in config.per_op.  The K steps are timed op-major:
+each op's K calls run back to back, bracketed by one pair of HIP events on the stream the
+kernels run on, so every op pays for its own cache write-backs and an op's time is that
+span over K.  Each op cycles through enough buffer sets that the working set between two
+uses of a set exceeds 1 GB, so the 256 MB MALL cannot serve repeats.  Algorithmic bytes
+count every input read once and every output written once.
 
 cpu_baseline: the oracle's float pipeline (oracle/, OpenMP) on a row sample of every op,
 timed on this host's cores.
@@ -24,11 +25,11 @@ timed on this host's cores.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
 import re
-import statistics
 import sys
 import time
 from pathlib import Path
@@ -66,7 +67,8 @@ class Op:
         self.flops = 0.0
         self.next = False
         self.run = None          # (buffer set) -> None
-        self.times_ms = []
+        self.ms = 0.0            # mean GPU time per call over the timed calls
+        self.retimed = 0         # timings redone because the host enqueue outlasted the hold
 
 
 def build_ops(torch, mbrt, bands):
@@ -326,52 +328,63 @@ def main():
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
 
-    # Op-major order: every op runs its K calls back to back (each call bracketed by HIP
-    # events on the stream the kernels run on), so an op's time includes the write-back of
-    # the dirty lines its own previous call left in the MALL, not those of a different op.
-    def run_op(op, i, record):
-        b = op.sets[i % len(op.sets)]
-        if not record:
-            op.run(b)
-            return None
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        op.run(b)
-        e1.record(stream)
-        return e0, e1
-
-    # The host enqueues an op's K calls while the stream is held by a spin kernel of a few
-    # ms, so the calls then run back to back on the GPU and the events time the kernels,
-    # not the Python launch path (a ctypes call costs ~10 us, as long as the smaller ops).
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # Op-major order: every op runs its K calls back to back, so an op's time includes the
+    # write-back of the dirty lines its own previous call left in the MALL, not those of a
+    # different op.  One HIP event pair on the kernels' stream brackets an op's K calls and
+    # the op's time is that span over K: no events sit between the calls, as in a pipeline
+    # (the reference's own benchmark reports time over N calls the same way).
+    #
+    # The host enqueues the K calls while the stream is held by a spin kernel, so that they
+    # run back to back on the GPU and the events time the kernels, not the Python launch path
+    # (a ctypes call costs ~10 us, as long as the smaller ops).  Python's garbage collector is
+    # off meanwhile, and should the enqueue still take more than half the hold, the op is
+    # timed again with a longer hold: no GPU idle time can then fall inside the span.
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda._sleep(1 << 20)
-    e0.record(stream)
+    c0.record(stream)
     torch.cuda._sleep(1 << 20)
-    e1.record(stream)
+    c1.record(stream)
     torch.cuda.synchronize()
-    hold_cycles = int((1 << 20) * max(1.0, (2.0 + 0.3 * args.steps) / max(e0.elapsed_time(e1), 1e-3)))
+    ms_per_unit = max(c0.elapsed_time(c1), 1e-3)  # GPU ms of a 2^20-cycle spin
+
+    def time_op(op):
+        hold_ms = 2.0 + 0.3 * args.steps
+        for attempt in range(4):
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            gc.disable()
+            try:
+                torch.cuda._sleep(int((1 << 20) * max(1.0, hold_ms / ms_per_unit)))
+                h0 = time.perf_counter()
+                a0.record(stream)
+                for i in range(args.steps):
+                    op.run(op.sets[(args.warmup + i) % len(op.sets)])
+                a1.record(stream)
+                enqueue_ms = (time.perf_counter() - h0) * 1e3
+            finally:
+                gc.enable()
+            torch.cuda.synchronize()
+            if enqueue_ms < 0.5 * hold_ms:
+                op.ms = a0.elapsed_time(a1) / args.steps
+                op.retimed = attempt
+                return
+            hold_ms *= 4
+        raise RuntimeError(f"bench.py: the host could not enqueue {op.name} within the stream hold")
 
     for op in ops:
         for i in range(args.warmup):
-            run_op(op, i, False)
+            op.run(op.sets[i % len(op.sets)])
     torch.cuda.synchronize()
-    all_evs = []
     t0 = time.perf_counter()
     for op in ops:
-        torch.cuda._sleep(hold_cycles)
-        for i in range(args.steps):
-            all_evs.append((op, run_op(op, args.warmup + i, True)))
-    torch.cuda.synchronize()
+        time_op(op)
     wall = time.perf_counter() - t0
-    for op, (e0, e1) in all_evs:
-        op.times_ms.append(e0.elapsed_time(e1))
 
     per_op = {}
     next_ops = {}
     tot_bytes = 0
     tot_ms = 0.0
     for op in [o for o in ops if o.next]:
-        ms = statistics.mean(op.times_ms)
+        ms = op.ms
         gbs = op.bytes / (ms * 1e-3) / 1e9
         if op.flops > 0:
             tf = op.flops / (ms * 1e-3) / 1e12
@@ -383,11 +396,13 @@ def main():
                                  "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "kernel": op.kernel}
     ops = [o for o in ops if not o.next]
     for op in ops:
-        ms = statistics.mean(op.times_ms)
+        ms = op.ms
         gbs = op.bytes / (ms * 1e-3) / 1e9
-        per_op[op.name] = {"bytes": op.bytes, "ms": round(ms, 5), "median_ms": round(statistics.median(op.times_ms), 5),
+        per_op[op.name] = {"bytes": op.bytes, "ms": round(ms, 5),
                            "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                            "buffer_sets": len(op.sets), "kernel": op.kernel}
+        if op.retimed:
+            per_op[op.name]["retimed"] = op.retimed
         if gbs > HBM_PEAK_GBS:  # inputs are cycled past the MALL: this can only be a measurement error
             print(f"bench.py: {op.name} reports {gbs:.0f} GB/s, above the HBM peak", file=sys.stderr)
             per_op[op.name]["suspect"] = True
@@ -396,8 +411,8 @@ def main():
     if not ops:  # a tuning run of next_ops only
         print(json.dumps({"config": {"next_ops": next_ops}}), flush=True)
         return
-    dom = max(ops, key=lambda o: statistics.mean(o.times_ms))
-    dom_ms = statistics.mean(dom.times_ms)
+    dom = max(ops, key=lambda o: o.ms)
+    dom_ms = dom.ms
     achieved = dom.bytes / (dom_ms * 1e-3) / 1e9
     value = tot_bytes / (tot_ms * 1e-3) / 1e9
 
@@ -425,9 +440,10 @@ def main():
             "workload": "mbr_chunk_tensor_ops: BL-1..BL-5 at full MelBandRoformer chunk shape "
                         "(T=801 frames, 60 bands, D=384, batch 4 band split), one pass per step",
             "ms_tensor_ops_per_step": round(tot_ms, 4),
-            "ms_per_step_note": "GPU time of one pass over all ops (sum of per-op event means); the "
-                                "timed region's wall clock, which also holds the host-side holds, is "
-                                "wall_ms_per_step",
+            "ms_per_step_note": "GPU time of one pass over all ops (sum of per-op means, each one "
+                                "HIP event pair over the op's K back-to-back calls); the timed "
+                                "region's wall clock, which also holds the stream holds and "
+                                "synchronisations, is wall_ms_per_step",
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
             "frac_hbm_peak_all_ops": round(value / HBM_PEAK_GBS, 4),
             "storage_dtypes": "f32 and bf16 per op name; all arithmetic in f32",
