@@ -172,6 +172,24 @@ def build_ops(torch, mbrt, bands):
         op.next = True
         op.run = lambda b: mbrt.attention(b["q"], b["k"], b["v"], b["y"], 0.125)
         ops.append(op)
+    # The time attention as the reference's split-contig q-rotary form plus the gate: q, k, v
+    # read in place from the fused qkv projection [60, 801, 3*8*64], q rotated in the kernel,
+    # the sigmoid gate [60, 801, 8] and the head merge applied in the epilogue -> [60, 801, 512].
+    # It replaces rotary-on-q + the split + attention + gate merge.
+    Bq, Nq, Hq = 60, 801, 8
+    cos_t, sin_t = (torch.from_numpy(t).to(dev) for t in mbrt.rotary_tables(Nq, 64))
+    op = Op("attention_time_fused_qrot_gate_bf16", Bq * Nq * 3 * Hq * 64 * 2 + Bq * Nq * Hq * 2 + Bq * Nq * Hq * 64 * 2,
+            lambda: dict(qkv=randn((Bq, Nq, 3 * Hq * 64), bf16), g=randn((Bq, Nq, Hq), bf16, std=2.0),
+                         y=torch.empty((Bq, Nq, Hq * 64), dtype=bf16, device=dev)),
+            "attention_kernel")
+    op.flops = 4.0 * Bq * Hq * Nq * Nq * 64
+    op.next = True
+
+    def run_fused(b):
+        q5 = b["qkv"].view(Bq, Nq, 3, Hq, 64)
+        mbrt.attention_bnhd(q5[:, :, 0], q5[:, :, 1], q5[:, :, 2], b["y"], 0.125, cos=cos_t, sin=sin_t, gate=b["g"])
+    op.run = run_fused
+    ops.append(op)
     # STFT / iSTFT (n_fft 2048, hop 441, Hann, centred) of the chunk: 4 x 2 channels x 352800
     # samples <-> [8, 1025, 801, 2].  Memory-bound; reported in config.next_ops with GB/s of
     # algorithmic bytes (signal + spectrum; the iSTFT's frame workspace is not counted).

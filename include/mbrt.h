@@ -328,6 +328,29 @@ MBRT_API int mbrt_attention(const void* q, const void* k, const void* v, int dty
                             int64_t BH, int64_t n_q, int64_t n_k, int64_t head_dim, float scale,
                             mbrt_stream_t stream);
 
+/* The same attention over strided q, k, v, with optional in-kernel rotary of q and an
+ * optional sigmoid-gate head-merge epilogue.  Head (b, h) of B x H, row n, element d sits
+ * at q + b*q_batch_stride + h*q_head_stride + n*q_row_stride + d (k and v with the kv
+ * strides; every stride a non-negative multiple of 8 elements).  [B, N, H, 64] views of a
+ * fused qkv projection are strides (N*3*H*64, 64, 3*H*64).
+ *  - rot_cos / rot_sin [n_q, 32] (F32/BF16, NULL for none): q row n is rotated as
+ *    mbrt_rotary_inplace would (pairs (2i, 2i+1), f32, rounded to bf16) before use.
+ *  - gate [B, n_q, H] (F32/BF16/F16, NULL for none): out is [B, n_q, H*64] with
+ *    out[b, n, h*64 + d] = O * g, g = sigmoid(gate) when gate_is_logit, O first rounded
+ *    to out_dtype: the result equals mbrt_sigmoid_gate_merge of the plain output.  Without
+ *    a gate, out is [B*H, n_q, 64].
+ * Replaces mbr_tile::scaled_dot_product_attention_time_split_contig[_q_rotary]
+ * (src/mbr_cuda_tile.cu:6417-6527; kernels src/mbr_time_attention_cutile.cu:403-542),
+ * generalised from N = 1301 and scale 1/8, and fuses apply_gates_and_merge_heads
+ * (src/mbr_cuda_tile.cu:6243-6295) into the epilogue. */
+MBRT_API int mbrt_attention_strided(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                                    int64_t n_q, int64_t n_k, int64_t head_dim, int64_t q_batch_stride,
+                                    int64_t q_head_stride, int64_t q_row_stride, int64_t kv_batch_stride,
+                                    int64_t kv_head_stride, int64_t kv_row_stride, const void* rot_cos,
+                                    const void* rot_sin, int trig_dtype, const void* gate, int gate_dtype,
+                                    int gate_is_logit, void* out, int out_dtype, float scale,
+                                    mbrt_stream_t stream);
+
 /* ---- STFT / iSTFT (n_fft = win_length = 2048) --------------------------------- */
 
 /* Hann window of `size` f32 samples, 0.5 (1 - cos(2 pi n / size)) in f32; size 1 gives

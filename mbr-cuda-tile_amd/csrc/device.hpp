@@ -378,6 +378,20 @@ __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcp
 
 __device__ __forceinline__ float sigmoidf(float x) { return fast_rcp(1.0f + fast_exp(-x)); }
 
+// Rotary rotation of a pair: (x0, x1) -> (x0 c - x1 s, x0 s + x1 c), each product and the
+// sum rounded separately (no FMA contraction), so that every kernel that rotates (the rotary
+// kernels, the qkv split, the attention's in-kernel q rotation) rounds alike.
+__device__ __forceinline__ void rotate_pair(float x0, float x1, float c, float s, float& y0, float& y1) {
+#pragma clang fp contract(off)
+    y0 = x0 * c - x1 * s;
+    y1 = x0 * s + x1 * c;
+}
+template <int VE>
+__device__ __forceinline__ void rotate(float (&x)[VE], const float (&c)[VE / 2], const float (&s)[VE / 2]) {
+#pragma unroll
+    for (int i = 0; i < VE / 2; ++i) rotate_pair(x[2 * i], x[2 * i + 1], c[i], s[i], x[2 * i], x[2 * i + 1]);
+}
+
 // GELU in the reference's form 0.5 x (1 + erf(x)) (mode 1) and the standard
 // 0.5 x (1 + erf(x / sqrt 2)) (mode 2), both written as 0.5 x erfc(-z) so that the
 // negative tail keeps full relative precision (1 + erf(z) cancels for z << 0).

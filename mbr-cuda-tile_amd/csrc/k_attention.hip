@@ -59,6 +59,8 @@ __device__ __forceinline__ int tile_at(int r, int chunk, int within) {
     return r * kHeadDim + 8 * (chunk ^ (r & 7)) + within;
 }
 
+// Element (bh, n, d) of q sits at q + b q_bs + h q_hs + n q_rs + d, with b = bh / H and
+// h = bh % H; k and v likewise with the kv strides.  Contiguous [BH, N, 64] is H = 1.
 struct AttnArgs {
     const __bf16* q;
     const __bf16* k;
@@ -67,6 +69,15 @@ struct AttnArgs {
     int nq, nk;
     uint32_t qtiles;
     float scale_log2e;
+    FastDiv heads;
+    int64_t q_bs, q_hs, kv_bs, kv_hs;
+    int q_rs, kv_rs;
+    const void* cosp;   // q rotary tables [n_q, 32] of dtype tdt, or NULL: q used as given
+    const void* sinp;
+    int tdt;
+    const void* gate;   // gate [B, n_q, H] of dtype gdt, or NULL: out [BH, n_q, 64]
+    int gdt;
+    int glogit;         // the gate holds logits: sigmoid(gate) multiplies
 };
 
 __device__ __forceinline__ float xor_max(float x) {
@@ -96,18 +107,54 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
     // XCD walks one contiguous range of it, so that the query tiles of a (b, h) run on one
     // XCD, close in time, and read its K/V once into that XCD's L2
     const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
-    const int64_t bh = tile / a.qtiles;
+    const uint32_t bh = tile / a.qtiles;
     const int q0 = (tile % a.qtiles) * kQB + w * kQWave * QS;
-    const __bf16* kbase = a.k + bh * a.nk * kHeadDim;
-    const __bf16* vbase = a.v + bh * a.nk * kHeadDim;
+    uint32_t b, h;
+    fdivmod(bh, a.heads, b, h);
+    const __bf16* kbase = a.k + b * a.kv_bs + h * a.kv_hs;
+    const __bf16* vbase = a.v + b * a.kv_bs + h * a.kv_hs;
 
     // Q fragments: for sub-block x, lane holds Q[q0 + 16x + c][32s + 8g .. +7], s = 0, 1
     bf16x8 qf[QS][2];
 #pragma unroll
     for (int x = 0; x < QS; ++x) {
-        const __bf16* qrow = a.q + (bh * a.nq + min(q0 + 16 * x + c, a.nq - 1)) * kHeadDim;
+        const __bf16* qrow = a.q + b * a.q_bs + h * a.q_hs + (int64_t)min(q0 + 16 * x + c, a.nq - 1) * a.q_rs;
 #pragma unroll
         for (int s = 0; s < 2; ++s) qf[x][s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
+    }
+    if (a.cosp != nullptr) {
+        // in-kernel rotary of q: the lane's 8 values are the pairs 16s + 4g .. +3 of its query
+        // row, rotated by the shared rotate() in f32 and rounded to bf16 as the rotary kernel
+        // does (src/mbr_time_attention_cutile.cu:80-106, 489-490)
+#pragma unroll
+        for (int x = 0; x < QS; ++x) {
+            const int64_t t = (int64_t)min(q0 + 16 * x + c, a.nq - 1) * (kHeadDim / 2);
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                float cs[4], sn[4];
+                if (a.tdt == F32) {
+                    Vec<F32, 4> cv, sv;
+                    cv.load(a.cosp, t + 16 * s + 4 * g);
+                    sv.load(a.sinp, t + 16 * s + 4 * g);
+                    cv.to_f32(cs);
+                    sv.to_f32(sn);
+                } else {
+                    Vec<BF16, 4> cv, sv;
+                    cv.load(a.cosp, t + 16 * s + 4 * g);
+                    sv.load(a.sinp, t + 16 * s + 4 * g);
+                    cv.to_f32(cs);
+                    sv.to_f32(sn);
+                }
+                Vec<BF16, 8> qv;
+                const u32x4 qw = __builtin_bit_cast(u32x4, qf[x][s]);
+                qv.w[0] = qw.x; qv.w[1] = qw.y; qv.w[2] = qw.z; qv.w[3] = qw.w;
+                float xv[8];
+                qv.to_f32(xv);
+                rotate<8>(xv, cs, sn);
+                qv.from_f32(xv);
+                qf[x][s] = __builtin_bit_cast(bf16x8, u32x4{qv.w[0], qv.w[1], qv.w[2], qv.w[3]});
+            }
+        }
     }
 
     f32x4 o[QS][4];
@@ -131,7 +178,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int r0 = 16 * w + 8 * u, key = r0 + (lane >> 3);
-            const uint32_t off = (uint32_t)min(kt + key, a.nk - 1) * kHeadDim + 8 * ((lane & 7) ^ (lane >> 3));
+            const uint32_t off = (uint32_t)min(kt + key, a.nk - 1) * a.kv_rs + 8 * ((lane & 7) ^ (lane >> 3));
             __builtin_amdgcn_global_load_lds((global_void*)(kbase + off), (lds_void*)&kd[r0 * kHeadDim], 16, 0, 0);
             __builtin_amdgcn_global_load_lds((global_void*)(vbase + off), (lds_void*)&vd[r0 * kHeadDim], 16, 0, 0);
         }
@@ -260,7 +307,30 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
         const int q = q0 + 16 * x + c;
         if (q >= a.nq) continue;
         const float inv = 1.0f / lsum;
-        const int64_t obase = (bh * a.nq + q) * kHeadDim;
+        if (a.gate != nullptr) {
+            // gate and head merge: merged[b, q, h*64 + d] = O * g(b, q, h), O first rounded to
+            // the output dtype, so that the result equals the attention output passed through
+            // mbrt_sigmoid_gate_merge
+            const int64_t tok = ((int64_t)b * a.nq + q) * a.heads.d + h;
+            const float gl = load1(a.gate, a.gdt, tok);
+            const float gv = a.glogit ? sigmoidf(gl) : gl;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const int64_t e = tok * kHeadDim + 16 * db + 4 * g;
+                if constexpr (ODT == F32) {
+                    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + e) = (o[x][db] * inv) * gv;
+                } else {
+                    const uint32_t r0 = pack_bf16x2(o[x][db][0] * inv, o[x][db][1] * inv);
+                    const uint32_t r1 = pack_bf16x2(o[x][db][2] * inv, o[x][db][3] * inv);
+                    u32x2 pk;
+                    pk.x = pack_bf16x2(bf16_lo(r0) * gv, bf16_hi(r0) * gv);
+                    pk.y = pack_bf16x2(bf16_lo(r1) * gv, bf16_hi(r1) * gv);
+                    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + e) = pk;
+                }
+            }
+            continue;
+        }
+        const int64_t obase = ((int64_t)bh * a.nq + q) * kHeadDim;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
             const int d = 16 * db + 4 * g;
@@ -283,21 +353,45 @@ using namespace mbrt;
 
 extern "C" {
 
-int mbrt_attention(const void* q, const void* k, const void* v, int dtype, void* out, int out_dtype, int64_t BH,
-                   int64_t n_q, int64_t n_k, int64_t head_dim, float scale, mbrt_stream_t stream) {
+int mbrt_attention_strided(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t n_q,
+                           int64_t n_k, int64_t head_dim, int64_t q_batch_stride, int64_t q_head_stride,
+                           int64_t q_row_stride, int64_t kv_batch_stride, int64_t kv_head_stride,
+                           int64_t kv_row_stride, const void* rot_cos, const void* rot_sin, int trig_dtype,
+                           const void* gate, int gate_dtype, int gate_is_logit, void* out, int out_dtype,
+                           float scale, mbrt_stream_t stream) {
     const char* op = "mbrt_attention";
     MBRT_REQUIRE(dtype == BF16, MBRT_E_UNSUPPORTED_DTYPE, "%s: q/k/v must be BF16", op);
     MBRT_REQUIRE(out_dtype == BF16 || out_dtype == F32, MBRT_E_UNSUPPORTED_DTYPE, "%s: out must be BF16/F32", op);
     MBRT_REQUIRE(head_dim == kHeadDim, MBRT_E_SHAPE, "%s: head_dim %lld (only 64 is built)", op, (long long)head_dim);
-    MBRT_REQUIRE(BH >= 0 && n_q >= 0 && n_k >= 0, MBRT_E_SHAPE, "%s: bad shape", op);
-    if (BH == 0 || n_q == 0) return MBRT_OK;
+    MBRT_REQUIRE(B >= 0 && H >= 1 && n_q >= 0 && n_k >= 0, MBRT_E_SHAPE, "%s: bad shape", op);
+    if (B == 0 || n_q == 0) return MBRT_OK;
     MBRT_REQUIRE(n_k >= 1, MBRT_E_SHAPE, "%s: attention over zero keys", op);
-    MBRT_REQUIRE(n_q < (1 << 24) && n_k < (1 << 24), MBRT_E_SHAPE, "%s: sequence longer than 2^24", op);
+    MBRT_REQUIRE(n_q < (1 << 24) && n_k < (1 << 24) && H < (1 << 24), MBRT_E_SHAPE, "%s: dimension beyond 2^24", op);
     MBRT_REQUIRE(q && k && v && out, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
     MBRT_REQUIRE(scale >= 0.0f && std::isfinite(scale), MBRT_E_INVALID_ARG, "%s: scale must be finite and >= 0", op);
     MBRT_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16), MBRT_E_ALIGN,
                  "%s: q, k, v and out must be 16-byte aligned", op);
-    MBRT_REQUIRE(BH * ceil_div(n_q, kQBlock) < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many tiles", op);
+    // rows are read in 16-byte pieces: every stride a multiple of 8 elements, rows of 64
+    const int64_t st[6] = {q_batch_stride, q_head_stride, q_row_stride, kv_batch_stride, kv_head_stride, kv_row_stride};
+    for (int i = 0; i < 6; ++i)
+        MBRT_REQUIRE(st[i] >= 0 && st[i] % 8 == 0, MBRT_E_ALIGN, "%s: strides must be non-negative multiples of 8", op);
+    MBRT_REQUIRE(q_row_stride >= kHeadDim && kv_row_stride >= kHeadDim, MBRT_E_SHAPE, "%s: row stride below head_dim",
+                 op);
+    // key offsets within one (b, h) are 32-bit
+    MBRT_REQUIRE((n_k - 1) * kv_row_stride + kHeadDim < (int64_t(1) << 31), MBRT_E_SHAPE,
+                 "%s: k/v rows of one head span 2^31 elements", op);
+    MBRT_REQUIRE((rot_cos == nullptr) == (rot_sin == nullptr), MBRT_E_INVALID_ARG, "%s: give both cos and sin", op);
+    if (rot_cos) {
+        MBRT_REQUIRE(trig_dtype == F32 || trig_dtype == BF16, MBRT_E_UNSUPPORTED_DTYPE, "%s: cos/sin must be F32/BF16",
+                     op);
+        MBRT_REQUIRE(aligned(rot_cos, trig_dtype == F32 ? 16 : 8) && aligned(rot_sin, trig_dtype == F32 ? 16 : 8),
+                     MBRT_E_ALIGN, "%s: cos/sin tables must be aligned to 4 elements", op);
+    }
+    if (gate) {
+        MBRT_REQUIRE(gate_dtype == F32 || gate_dtype == BF16 || gate_dtype == F16, MBRT_E_UNSUPPORTED_DTYPE,
+                     "%s: gate must be F32/BF16/F16", op);
+    }
+    const int64_t BH = B * H;
     AttnArgs a{};
     a.q = static_cast<const __bf16*>(q);
     a.k = static_cast<const __bf16*>(k);
@@ -306,19 +400,42 @@ int mbrt_attention(const void* q, const void* k, const void* v, int dtype, void*
     a.nq = (int)n_q;
     a.nk = (int)n_k;
     a.scale_log2e = (scale == 0.0f ? 1.0f / std::sqrt((float)head_dim) : scale) * 1.44269504088896340736f;
+    a.heads = make_fastdiv((uint32_t)H);
+    a.q_bs = q_batch_stride;
+    a.q_hs = q_head_stride;
+    a.kv_bs = kv_batch_stride;
+    a.kv_hs = kv_head_stride;
+    MBRT_REQUIRE(q_row_stride < (int64_t(1) << 31) && kv_row_stride < (int64_t(1) << 31), MBRT_E_SHAPE,
+                 "%s: row stride beyond 2^31", op);
+    a.q_rs = (int)q_row_stride;
+    a.kv_rs = (int)kv_row_stride;
+    a.cosp = rot_cos;
+    a.sinp = rot_sin;
+    a.tdt = trig_dtype;
+    a.gate = gate;
+    a.gdt = gate_dtype;
+    a.glogit = gate_is_logit ? 1 : 0;
     // two query sub-blocks per wave once a (b, h) has more than one workgroup of queries
     const int qs = n_q > kQBlock * MBRT_ATTN_QS2_MIN ? 2 : 1;
     a.qtiles = (uint32_t)ceil_div(n_q, (int64_t)kQBlock * qs);
+    MBRT_REQUIRE(BH * a.qtiles < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many tiles", op);
     const dim3 grid((unsigned)(BH * a.qtiles));
-    hipStream_t st = as_stream(stream);
+    hipStream_t stm = as_stream(stream);
     if (qs == 2) {
-        if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 2>), grid, dim3(kWaves * 64), 0, st, a);
-        else hipLaunchKernelGGL((attention_kernel<F32, 2>), grid, dim3(kWaves * 64), 0, st, a);
+        if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 2>), grid, dim3(kWaves * 64), 0, stm, a);
+        else hipLaunchKernelGGL((attention_kernel<F32, 2>), grid, dim3(kWaves * 64), 0, stm, a);
     } else {
-        if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 1>), grid, dim3(kWaves * 64), 0, st, a);
-        else hipLaunchKernelGGL((attention_kernel<F32, 1>), grid, dim3(kWaves * 64), 0, st, a);
+        if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 1>), grid, dim3(kWaves * 64), 0, stm, a);
+        else hipLaunchKernelGGL((attention_kernel<F32, 1>), grid, dim3(kWaves * 64), 0, stm, a);
     }
     return check_launch(op);
+}
+
+int mbrt_attention(const void* q, const void* k, const void* v, int dtype, void* out, int out_dtype, int64_t BH,
+                   int64_t n_q, int64_t n_k, int64_t head_dim, float scale, mbrt_stream_t stream) {
+    return mbrt_attention_strided(q, k, v, dtype, BH, 1, n_q, n_k, head_dim, n_q * head_dim, 0, head_dim,
+                                  n_k * head_dim, 0, head_dim, nullptr, nullptr, F32, nullptr, F32, 0, out, out_dtype,
+                                  scale, stream);
 }
 
 }  // extern "C"

@@ -31,16 +31,6 @@ struct RotArgs {
     FastDiv heads_div;
 };
 
-template <int VE>
-__device__ __forceinline__ void rotate(float (&x)[VE], const float (&c)[VE / 2], const float (&s)[VE / 2]) {
-#pragma unroll
-    for (int i = 0; i < VE / 2; ++i) {
-        const float x0 = x[2 * i], x1 = x[2 * i + 1];
-        x[2 * i] = x0 * c[i] - x1 * s[i];
-        x[2 * i + 1] = x0 * s[i] + x1 * c[i];
-    }
-}
-
 // One thread = one VE-element group (VE/2 pairs) of q and the same group of k.  All four
 // loads (q, k, cos, sin) are issued before the rotation.
 template <int DT, int TDT, bool HAS_K>
@@ -90,8 +80,10 @@ __global__ __launch_bounds__(kThreads) void rotary_scalar_kernel(RotArgs a) {
             void* buf = t == 0 ? a.q : a.k;
             if (buf == nullptr) continue;
             const float x0 = load1(buf, a.dt, e), x1 = load1(buf, a.dt, e + 1);
-            store1(buf, a.dt, e, x0 * c - x1 * s);
-            store1(buf, a.dt, e + 1, x0 * s + x1 * c);
+            float y0, y1;
+            rotate_pair(x0, x1, c, s, y0, y1);
+            store1(buf, a.dt, e, y0);
+            store1(buf, a.dt, e + 1, y1);
         }
     }
 }
@@ -171,8 +163,10 @@ __global__ __launch_bounds__(kThreads) void split_qkv_scalar_kernel(SplitArgs a)
                 const float x0 = load1(a.qkv, a.idt, src + part * a.H * a.D);
                 const float x1 = load1(a.qkv, a.idt, src + part * a.H * a.D + 1);
                 if (part < 2) {
-                    store1(dst, a.odt, e, x0 * c - x1 * s);
-                    store1(dst, a.odt, e + 1, x0 * s + x1 * c);
+                    float y0, y1;
+                    rotate_pair(x0, x1, c, s, y0, y1);
+                    store1(dst, a.odt, e, y0);
+                    store1(dst, a.odt, e + 1, y1);
                 } else {
                     store1(dst, a.odt, e, x0);
                     store1(dst, a.odt, e + 1, x1);

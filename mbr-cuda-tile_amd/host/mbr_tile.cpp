@@ -4,6 +4,7 @@
 #include "mbr_tile.h"
 
 #include <algorithm>
+#include <limits>
 #include <stdexcept>
 #include <string>
 
@@ -207,6 +208,54 @@ Tensor scaled_dot_product_attention(const Tensor& q, const Tensor& k, const Tens
                              Nk, D, scale, abi_stream()),
               op);
     return out;
+}
+
+namespace {
+// The reference's split-contig time attention (src/mbr_cuda_tile.cu:6417-6527): q, k, v
+// [B, N, H, D] bf16 with unit inner stride, read through their strides.
+Tensor split_contig_attention(const char* op, const Tensor& q, const Tensor& k, const Tensor& v, const Tensor* cos_f,
+                              const Tensor* sin_f, float scale) {
+    if (q.dtype() != DType::BFloat16 || k.dtype() != DType::BFloat16 || v.dtype() != DType::BFloat16)
+        throw std::runtime_error(std::string(op) + ": expected BF16 q/k/v");
+    if (q.ndim() != 4 || k.shape() != q.shape() || v.shape() != q.shape())
+        throw std::runtime_error(std::string(op) + ": expected q/k/v [B, N, H, D] of one shape");
+    const int64_t B = q.size(0), N = q.size(1), H = q.size(2), D = q.size(3);
+    if (B <= 0 || B * H > std::numeric_limits<int>::max())
+        throw std::runtime_error(std::string(op) + ": invalid batch count");
+    auto inner = [](const Tensor& t) { return t.strides()[3] == 1 ? t : t.contiguous(); };
+    Tensor qb = inner(q), kb = inner(k), vb = inner(v);
+    if (kb.strides() != vb.strides()) vb = vb.contiguous(), kb = kb.contiguous();
+    Tensor cw, sw;
+    if (cos_f) {
+        if (cos_f->ndim() != 2 || sin_f->ndim() != 2 || cos_f->size(0) != N || sin_f->size(0) != N ||
+            cos_f->size(1) != D / 2 || sin_f->size(1) != D / 2)
+            throw std::runtime_error(std::string(op) + ": expected cos/sin [N, D/2]");
+        const bool bf = cos_f->dtype() == DType::BFloat16 && sin_f->dtype() == DType::BFloat16;
+        cw = bf ? cos_f->contiguous() : (cos_f->dtype() == DType::Float32 ? cos_f->contiguous() : cos_f->to_f32().contiguous());
+        sw = bf ? sin_f->contiguous() : (sin_f->dtype() == DType::Float32 ? sin_f->contiguous() : sin_f->to_f32().contiguous());
+    }
+    Tensor out = Tensor::empty({B, H, N, D}, DType::BFloat16);
+    abi_check(mbrt_attention_strided(qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), MBRT_BF16, B, H, N, N, D,
+                                     qb.strides()[0], qb.strides()[2], qb.strides()[1], kb.strides()[0],
+                                     kb.strides()[2], kb.strides()[1],
+                                     cos_f ? cw.data_ptr() : nullptr, cos_f ? sw.data_ptr() : nullptr,
+                                     cos_f ? code(cw.dtype()) : MBRT_F32, nullptr, MBRT_F32, 0, out.data_ptr(),
+                                     MBRT_BF16, scale, abi_stream()),
+              op);
+    return out;
+}
+}  // namespace
+
+Tensor scaled_dot_product_attention_time_split_contig(const Tensor& q, const Tensor& k, const Tensor& v, float scale) {
+    return split_contig_attention("mbr_tile::scaled_dot_product_attention_time_split_contig", q, k, v, nullptr,
+                                  nullptr, scale);
+}
+
+Tensor scaled_dot_product_attention_time_split_contig_q_rotary(const Tensor& q, const Tensor& k, const Tensor& v,
+                                                               const Tensor& cos_freqs, const Tensor& sin_freqs,
+                                                               float scale) {
+    return split_contig_attention("mbr_tile::scaled_dot_product_attention_time_split_contig_q_rotary", q, k, v,
+                                  &cos_freqs, &sin_freqs, scale);
 }
 
 Tensor softmax_last_dim(const Tensor& x, float scale, DType out_dtype) {

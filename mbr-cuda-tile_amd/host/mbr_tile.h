@@ -56,6 +56,17 @@ Tensor apply_gate_logits_and_merge_heads(const Tensor& attn, const Tensor& gate_
 // BF16 under g_quantize_bf16, else F32.
 Tensor scaled_dot_product_attention(const Tensor& q, const Tensor& k, const Tensor& v, float scale);
 
+// Time attention straight from the split-contig projection layout: q, k, v [B, N, H, D]
+// bf16 (views of the fused qkv are read in place through their strides) -> [B, H, N, D]
+// bf16; the _q_rotary form rotates q in the kernel with cos/sin [N, D/2] (F32 or BF16;
+// other dtypes go to F32).  src/mbr_cuda_tile.cu:6417-6527, generalised from N = 1301,
+// H = 8 and scale 1/8 (0 still means 1/sqrt(D)).  Throws "expected BF16 q/k/v" and
+// shape errors as the reference does.
+Tensor scaled_dot_product_attention_time_split_contig(const Tensor& q, const Tensor& k, const Tensor& v, float scale);
+Tensor scaled_dot_product_attention_time_split_contig_q_rotary(const Tensor& q, const Tensor& k, const Tensor& v,
+                                                               const Tensor& cos_freqs, const Tensor& sin_freqs,
+                                                               float scale);
+
 // Row softmax of attention scores over the last dim, p = softmax(scale * x), f32
 // accumulation (the scale_softmax kernels, src/mbr_cuda_tile.cu:5092-5285).
 Tensor softmax_last_dim(const Tensor& x, float scale, DType out_dtype);

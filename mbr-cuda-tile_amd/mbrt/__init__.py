@@ -325,6 +325,37 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tens
     return out
 
 
+def attention_bnhd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None,
+                   scale: float = 0.0, cos: torch.Tensor | None = None, sin: torch.Tensor | None = None,
+                   gate: torch.Tensor | None = None, gate_is_logit: bool = True, out_dtype=None,
+                   stream=None) -> torch.Tensor:
+    """Fused attention over [B, N, H, 64] bf16 views (any strides with a unit last dim, e.g.
+    slices of a fused qkv projection).  cos, sin [n_q, 32] rotate q in-kernel.  Without a
+    gate the result is [B, H, n_q, 64]; with gate [B, n_q, H] it is the gated head merge
+    [B, n_q, H*64].  out_dtype defaults to bf16."""
+    B, nq, H, D = q.shape
+    nk = k.shape[1]
+    if k.shape != (B, nk, H, D) or v.shape != k.shape:
+        raise ValueError("attention_bnhd: expected q [B, N, H, D] and k, v [B, N_k, H, D]")
+    if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1 or k.stride() != v.stride():
+        raise ValueError("attention_bnhd: the last dim must be contiguous and k, v strided alike")
+    odt = out_dtype if out_dtype is not None else (out.dtype if out is not None else torch.bfloat16)
+    if out is None:
+        shape = (B, nq, H * D) if gate is not None else (B, H, nq, D)
+        out = torch.empty(shape, dtype=odt, device=q.device)
+    _contig(out)
+    for t in (cos, sin, gate):
+        if t is not None:
+            _contig(t)
+    _abi.call("mbrt_attention_strided", _p(q), _p(k), _p(v), dtype_code(q), B, H, nq, nk, D,
+              q.stride(0), q.stride(2), q.stride(1), k.stride(0), k.stride(2), k.stride(1),
+              _p(cos) if cos is not None else None, _p(sin) if sin is not None else None,
+              dtype_code(cos) if cos is not None else F32,
+              _p(gate) if gate is not None else None, dtype_code(gate) if gate is not None else F32,
+              int(gate_is_logit), _p(out), dtype_code(out), float(scale), _s(stream))
+    return out
+
+
 N_FFT = 2048
 
 

@@ -311,6 +311,12 @@ void ops(const std::string& path) {
         Tensor qa = I["q"].permute({0, 2, 1, 3}).contiguous();  // [B, H, N, D]
         Tensor ka = I["k"].permute({0, 2, 1, 3}).contiguous();
         d.save("attention", M::scaled_dot_product_attention(qa, ka, ka, 0.0f));
+        // the split-contig forms read [B, N, H, D] in place; the q-rotary one rotates q itself
+        d.save("attention_split_contig", M::scaled_dot_product_attention_time_split_contig(I["q"], I["k"], I["k"], 0.0f));
+        d.save("attention_split_contig_qrot",
+               M::scaled_dot_product_attention_time_split_contig_q_rotary(I["q"], k, k, I["cos"], I["sin"], 0.0f));
+        Tensor rqa = q.permute({0, 2, 1, 3}).contiguous(), rka = k.permute({0, 2, 1, 3}).contiguous();
+        d.save("attention_rotated", M::scaled_dot_product_attention(rqa, rka, rka, 0.0f));
     }
     Tensor sq, sk, sv;
     M::split_qkv_heads_rotary(I["qkv"], 8, 64, I["cos"], I["sin"], sq, sk, sv);

@@ -54,6 +54,8 @@ API = [
     "cudasep::mbr_tile::residual_bf16_enabled(", "cudasep::mbr_tile::bias_bf16_enabled(",
     "cudasep::mbr_tile::norm_gamma_bf16_enabled(", "cudasep::mbr_tile::bands_per_freq_bf16_enabled(",
     "cudasep::mbr_tile::rotary_freqs_bf16_enabled(", "cudasep::mbr_tile::scaled_dot_product_attention(",
+    "cudasep::mbr_tile::scaled_dot_product_attention_time_split_contig(",
+    "cudasep::mbr_tile::scaled_dot_product_attention_time_split_contig_q_rotary(",
     "cudasep::stft_tile::hann_window(", "cudasep::stft_tile::stft(", "cudasep::stft_tile::istft(",
     "cudasep::chunk_tile::accumulate_chunk(", "cudasep::chunk_tile::normalize_by_weights(",
     "cudasep::chunk_tile::process_chunked(",
@@ -196,6 +198,21 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
     den = orc.attention(orc.to_f32(qa, BF16), orc.to_f32(ka, BF16), np.abs(orc.to_f32(ka, BF16)), F32, F32,
                         0.0).reshape(B, H, N, Dh)
     assert_close(y, ref, BF16, "scaled_dot_product_attention", den=den)
+    # split-contig forms: the [B, N, H, D] views give the contiguous-heads result bit for bit,
+    # and the in-kernel q rotary equals rotating q first
+    dt, ys = _read(tmp_path, "attention_split_contig")
+    assert dt == BF16 and ys.shape == (B, H, N, Dh)
+    assert_bitexact(ys, y, "scaled_dot_product_attention_time_split_contig")
+    dt, yr = _read(tmp_path, "attention_split_contig_qrot")
+    assert dt == BF16 and yr.shape == (B, H, N, Dh)
+    assert_bitexact(yr, _read(tmp_path, "attention_rotated")[1], "scaled_dot_product_attention_time_split_contig_q_rotary")
+    gq, gk = _read(tmp_path, "rot_q")[1], _read(tmp_path, "rot_k")[1]
+    rqa = np.ascontiguousarray(gq.reshape(B, N, H, Dh).transpose(0, 2, 1, 3)).reshape(B * H, N, Dh)
+    rka = np.ascontiguousarray(gk.reshape(B, N, H, Dh).transpose(0, 2, 1, 3)).reshape(B * H, N, Dh)
+    ref_r = orc.attention(rqa, rka, rka, BF16, BF16, 0.0).reshape(B, H, N, Dh)
+    den_r = orc.attention(orc.to_f32(rqa, BF16), orc.to_f32(rka, BF16), np.abs(orc.to_f32(rka, BF16)), F32, F32,
+                          0.0).reshape(B, H, N, Dh)
+    assert_close(yr, ref_r, BF16, "split-contig q-rotary attention", den=den_r)
     sq, sk, sv = orc.split_qkv(qkv, BF16, cos, sin, F32, BF16, B, N, H, Dh, 64)
     for name, ref in (("split_q", sq), ("split_k", sk), ("split_v", sv)):
         dt, y = _read(tmp_path, name)

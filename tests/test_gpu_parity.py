@@ -593,6 +593,67 @@ def test_attention_full_shapes(orc, dev, BH, N, scale):
     print("attention full errors", assert_close(to_host(out[sel], BF16), ref, BF16, "attention", den=den))
 
 
+# Attention over [B, N, H, 64] views of a fused qkv projection, with the in-kernel q rotary
+# (the reference's split-contig _q_rotary form) and the gated head-merge epilogue: bit for
+# bit the separate GPU ops (rotary, attention, gate merge), and close to the oracle chain.
+@pytest.mark.parametrize("B,N,H,rot,gate,odt,tdt", [
+    (2, 801, 8, False, False, BF16, F32),
+    (2, 801, 8, True, False, BF16, F32),
+    (2, 70, 3, True, True, BF16, BF16),
+    (1, 60, 4, False, True, F32, F32),
+    (3, 130, 2, True, True, F32, F32),
+])
+def test_attention_bnhd_fusions(orc, dev, B, N, H, rot, gate, odt, tdt):
+    say(f"attention_bnhd B={B} N={N} H={H} rot={rot} gate={gate} out={odt} trig={tdt}")
+    tdt_torch = {F32: torch.float32, BF16: torch.bfloat16}
+    qkv = to_dev(inp(orc, (B, N, 3 * H * 64), 0x4D425200A3, N + H, BF16), BF16)
+    v5 = qkv.view(B, N, 3, H, 64)
+    q, k, v = v5[:, :, 0], v5[:, :, 1], v5[:, :, 2]  # strided views, read in place
+    cos_h, sin_h = orc.rotary_tables(N, 64)
+    if tdt == BF16:
+        cos_h, sin_h = orc.from_f32(cos_h, BF16), orc.from_f32(sin_h, BF16)
+    cos, sin = to_dev(cos_h, tdt), to_dev(sin_h, tdt)
+    g_h = inp(orc, (B, N, H), 0x4D425200A4, N, BF16, std=2.0)
+    g = to_dev(g_h, BF16)
+    fused = mbrt.attention_bnhd(q, k, v, cos=cos if rot else None, sin=sin if rot else None,
+                                gate=g if gate else None, out_dtype=tdt_torch[F32] if odt == F32 else torch.bfloat16)
+    # the separate ops on contiguous heads
+    qc, kc, vc = (t.permute(0, 2, 1, 3).contiguous().view(B * H, N, 64) for t in (q, k, v))
+    if rot:
+        mbrt.rotary_(qc, None, cos, sin)
+    att = empty((B, H, N, 64), odt)
+    mbrt.attention(qc, kc, vc, att.view(B * H, N, 64), 0.0)
+    sep = att
+    if gate:
+        sep = empty((B, N, H * 64), odt)
+        mbrt.gate_merge(att, g, sep)
+    torch.cuda.synchronize()
+    assert tuple(fused.shape) == tuple(sep.shape)
+    assert_bitexact(to_host(fused, odt), to_host(sep, odt), "attention_bnhd = separate ops")
+    # each stage against the oracle: the attention on the rotated q the rotary op produced
+    # (that op is pinned to the oracle itself), then the gate on that attention output (the
+    # two roundings of a chain may add up past one ulp of the final value)
+    qh, kh, vh = (to_host(t, BF16) for t in (qc, kc, vc))
+    ref = orc.attention(qh, kh, vh, BF16, odt, 0.0).reshape(B, H, N, 64)
+    den = orc.attention(orc.to_f32(qh, BF16), orc.to_f32(kh, BF16), np.abs(orc.to_f32(vh, BF16)), F32, F32,
+                        0.0).reshape(B, H, N, 64)
+    print("attention_bnhd errors", assert_close(to_host(att, odt), ref, odt, "attention_bnhd attention", den=den))
+    if gate:
+        gref = orc.gate_merge(to_host(att, odt), odt, g_h, BF16, odt, B, H, N, 64)
+        assert_close(to_host(fused, odt), gref, odt, "attention_bnhd gate merge")
+
+
+def test_attention_bnhd_rejects_bad_strides(dev):
+    t = torch.zeros((1, 16, 1, 68), dtype=torch.bfloat16, device="cuda")
+    q = t[..., :64]  # rows 68 elements apart: not 16-byte pieces
+    with pytest.raises(mbrt.MbrtError):
+        mbrt.attention_bnhd(q, q, q)
+    ok = torch.zeros((1, 16, 1, 64), dtype=torch.bfloat16, device="cuda")
+    cos = torch.zeros((16, 32), device="cuda")
+    with pytest.raises(mbrt.MbrtError):
+        mbrt.attention_bnhd(ok, ok, ok, cos=cos, sin=None)  # cos without sin
+
+
 def test_attention_rejects_bad_arguments(dev):
     q = torch.zeros((2, 8, 32), dtype=torch.bfloat16, device="cuda")
     out = torch.empty_like(q)
