@@ -90,6 +90,59 @@ def test_argument_errors_without_gpu(lib):
     assert lib.mbrt_rms_norm(null, 0, null, 0, null, 0, 10, 384, 1.0, 1e-12, null) == 1
 
 
+def test_widened_entry_points_reject_bad_arguments_without_gpu(lib):
+    """Attention, STFT / iSTFT and chunk entry points: each check fires before any launch.
+    Non-NULL pointers are fake 16-byte-aligned addresses that are never dereferenced."""
+    p = 0x10000   # aligned stand-in address
+    bf16, f32, f16 = 3, 0, 1
+
+    def strided(dtype=bf16, B=1, H=2, nq=8, nk=8, hd=64, q=(8 * 192, 64, 192), kv=(8 * 192, 64, 192),
+                cos=None, sin=None, gate=None, out_dtype=f32):
+        return lib.mbrt_attention_strided(p, p, p, dtype, B, H, nq, nk, hd, *q, *kv, cos, sin, f32, gate, bf16, 1,
+                                          p, out_dtype, 0.0, None)
+
+    assert strided(dtype=f32) == 2 and "BF16" in _err(lib)
+    assert strided(out_dtype=f16) == 2
+    assert strided(hd=32) == 3 and "head_dim" in _err(lib)
+    assert strided(B=0) == 0 and strided(nq=0) == 0          # nothing to do
+    assert strided(nk=0) == 3 and "zero keys" in _err(lib)
+    assert strided(q=(8 * 192, 64, 68)) == 4 and "multiples of 8" in _err(lib)
+    assert strided(kv=(8 * 192, 64, 32)) == 3 and "row stride" in _err(lib)
+    assert strided(cos=p) == 1 and "cos and sin" in _err(lib)
+    assert lib.mbrt_attention(p, p, p, bf16, p, f32, 4, 8, 8, 32, 0.0, None) == 3
+
+    def stft(batch=1, length=4096, n_fft=2048, hop=441, win=2048, numel=2048, center=1, sig=p, out=p):
+        return lib.mbrt_stft(sig, p, out, batch, length, n_fft, hop, win, numel, center, 0, None)
+
+    assert stft(n_fft=1024, win=1024, numel=1024) == 3
+    assert stft(hop=0) == 3
+    assert stft(length=2000, center=0) == 3 and "shorter than n_fft" in _err(lib)
+    assert stft(batch=0) == 0
+    assert stft(sig=None) == 1
+    assert stft(out=p + 4) == 4
+    assert lib.mbrt_stft_num_frames(4096, 441, 1) == 4096 // 441 + 1
+    assert lib.mbrt_stft_num_frames(4096, 441, 0) == (4096 - 2048) // 441 + 1
+
+    def istft(dtype=f32, bins=1025, frames=10, hop=441, batch=1, ws=None, ws_bytes=None):
+        need = lib.mbrt_istft_workspace_bytes(batch, frames, hop)
+        return lib.mbrt_istft(p, dtype, p, p, batch, bins, frames, 2048, hop, 2048, 2048, 1, 0, -1,
+                              p if ws is None else ws, need if ws_bytes is None else ws_bytes, None)
+
+    assert istft(bins=1024) == 3 and "1025" in _err(lib)
+    assert istft(dtype=f16) == 2
+    assert istft(hop=0) == 3
+    assert istft(batch=0) == 0
+    assert istft(ws_bytes=16) == 1 and "workspace" in _err(lib)
+    assert istft(ws=0) == 1
+
+    assert lib.mbrt_chunk_accumulate(p, p, p, p, 2, 100, 150, 60, None) == 3   # chunk past the end
+    assert lib.mbrt_chunk_accumulate(p, p, p, p, 0, 100, 150, 0, None) == 0
+    assert lib.mbrt_chunk_accumulate(p, None, p, p, 2, 100, 150, 0, None) == 1
+    assert lib.mbrt_chunk_normalize(None, p, 2, 100, None) == 1
+    assert lib.mbrt_chunk_fade_window(None, 100, 51, 0, 0) == 3               # fades overlap
+    assert lib.mbrt_hann_window(None, -1, None) == 3
+
+
 def test_empty_sizes_are_noops(lib):
     null = C.c_void_p(0)
     assert lib.mbrt_fill(null, 0, 0, 1.0, null) == 0
