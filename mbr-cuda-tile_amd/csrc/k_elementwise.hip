@@ -446,7 +446,7 @@ int mbrt_binary_broadcast(const void* a, const void* b, void* out, int dtype, co
         sa[0] = sb[0] = 0;
     }
     hipStream_t st = as_stream(stream);
-    bool small = total < (1ll << 32);
+    bool small = total < (1ll << 31);  // block * 256 + thread cannot wrap in 32 bits
     for (int d = 0; d < nd; ++d) small = small && shape[d] < (1ll << 31);
     dispatch_op(op_code, [&](auto opc) {
         constexpr int OP = decltype(opc)::value;

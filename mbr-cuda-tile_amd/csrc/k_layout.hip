@@ -145,7 +145,7 @@ int launch_row_copy(const char* src, char* dst, const Dims& dm, int esize, int64
     int64_t rows = 1;
     for (int d = 0; d < dm.nd - 1; ++d) rows *= dm.shape[d];
     const int64_t total = rows * vpr;
-    bool small = total < (1ll << 32) && vpr < (1ll << 31);
+    bool small = total < (1ll << 31) && vpr < (1ll << 31);  // 32-bit vector indices cannot wrap
     for (int d = 0; d < dm.nd - 1; ++d) small = small && dm.shape[d] < (1ll << 31);
     if (small) {
         RowCopyArgs a;

@@ -218,8 +218,10 @@ int mbrt_rotary_inplace(void* q, void* k, int dtype, const void* cos_table, cons
     const int64_t groups = rows * dim_head / ve;
     const uintptr_t tab_bytes = (uintptr_t)(ve / 2) * dt_size(trig_dtype);  // table bytes per group
     const bool tab_al = aligned(cos_table, tab_bytes) && aligned(sin_table, tab_bytes);
+    // the vector kernel indexes groups as block * 256 + thread in 32 bits: below 2^31 groups
+    // that sum cannot wrap onto a group another thread rotates (in place) as well
     const bool vec = dim_head % ve == 0 && aligned(q, 16) && (k == nullptr || aligned(k, 16)) && tab_al &&
-                     groups < (1ll << 32) && rows < (1ll << 31);
+                     groups < (1ll << 31) && rows < (1ll << 31);
     if (vec) {
         a.groups = (uint32_t)groups;
         a.gpr = make_fastdiv((uint32_t)(dim_head / ve));
@@ -278,7 +280,7 @@ int mbrt_split_qkv_heads_rotary(const void* qkv, int qkv_dtype, const void* cos_
     const uintptr_t tab_bytes = (uintptr_t)(ve / 2) * dt_size(trig_dtype);
     const bool tab_al = aligned(cos_table, tab_bytes) && aligned(sin_table, tab_bytes);
     const bool vec = D % ve == 0 && N >= 1 && aligned(qkv, 16) && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
-                     tab_al && groups < (1ll << 32);
+                     tab_al && groups < (1ll << 31);
     if (vec) {
         const dim3 grid((unsigned)ceil_div(groups, kThreads));
         const FastDiv gpr = make_fastdiv((uint32_t)(D / ve)), od = make_fastdiv((uint32_t)out_N),
