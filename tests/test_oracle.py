@@ -19,6 +19,7 @@ import torch
 from parity import BF16, F16, F32, assert_bitexact, assert_close
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
+I64, I32 = 2, 4  # the oracle's integer dtype ids
 
 
 # ---- rounding ----------------------------------------------------------------------------
@@ -97,6 +98,62 @@ def test_f64_to_bf16_single_rounding(orc):
     ref = np.array([_nearest_bf16_exact(v) if v >= 0 else _nearest_bf16_exact(-v) | 0x8000 for v in vals],
                    dtype=np.uint16)
     assert_bitexact(ours, ref, "f64->bf16")
+
+
+def _as_dtype(x: np.ndarray, dt: int) -> np.ndarray:
+    """numpy / torch conversion of float32 or integer values to oracle dtype `dt`."""
+    if dt == F32:
+        return x.astype(np.float32)
+    if dt == F16:
+        with np.errstate(over="ignore"):   # beyond 65504 rounds to inf, as intended
+            return x.astype(np.float32).astype(np.float16).view(np.uint16)
+    if dt == BF16:
+        return torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    return x.astype(np.int64 if dt == I64 else np.int32)
+
+
+def test_convert_every_dtype_pair_matches_numpy_and_torch(orc):
+    """convert_dtype (src/tensor_cuda_tile.cu:442-472): floats round to nearest even,
+    float -> integer truncates toward zero, integer -> float goes through f32 (RNE), and
+    i64 -> i32 keeps the low 32 bits.  Every pair against numpy / torch casts."""
+    rng = np.random.default_rng(4)
+    f = np.concatenate([rng.standard_normal(20_000) * 300.0, rng.standard_normal(2000) * 1e-3,
+                        np.array([-2.75, -2.5, -0.5, 0.0, 0.5, 2.5, 2.75, 65504.0, -65504.0, 1e6, -7.9999])])
+    f = f.astype(np.float32)
+    ints = np.concatenate([rng.integers(-2**40, 2**40, 5000), rng.integers(-70000, 70000, 5000),
+                           np.array([0, 1, -1, 2**24 + 1, -(2**24 + 1), 2**31 - 1, -2**31, 2**33 + 7])])
+    floats = (F32, F16, BF16)
+    for sdt in floats + (I64, I32):
+        for ddt in floats + (I64, I32):
+            if sdt in floats:
+                src = _as_dtype(f, sdt)
+                vals = orc.to_f32(src, sdt) if sdt != F32 else src   # the value the source holds
+                if ddt in floats:
+                    want = _as_dtype(vals, ddt)
+                else:
+                    small = np.abs(vals) < 2**31 - 128                  # in range of both integer types
+                    src, vals = _as_dtype(vals[small], sdt), vals[small]
+                    want = np.trunc(vals.astype(np.float64)).astype(np.int64 if ddt == I64 else np.int32)
+            else:
+                src = ints.astype(np.int64 if sdt == I64 else np.int32)
+                if ddt in floats:
+                    want = _as_dtype(src.astype(np.float32), ddt)     # through f32, then the float rule
+                else:
+                    want = src.astype(np.int64 if ddt == I64 else np.int32)
+            got = orc.convert(src, sdt, ddt)
+            assert_bitexact(np.asarray(got).view(want.dtype), want, f"convert {sdt}->{ddt}")
+
+
+@pytest.mark.parametrize("center", [True, False])
+def test_stft_num_frames_matches_torch(orc, center):
+    """Frame count of src/stft_cuda_tile.cu:544-551 against torch.stft's own output shape."""
+    w = torch.ones(2048, dtype=torch.float64)
+    for L in [2048, 2049, 3000, 4095, 4096, 9001, 20000] + ([1, 700, 1024, 2047] if center else []):
+        for hop in [1, 7, 441, 512, 1024, 2048, 3000]:
+            x = torch.zeros(L, dtype=torch.float64)
+            spec = torch.stft(x, 2048, hop, window=w, center=center, pad_mode="constant", return_complex=True)
+            assert orc.stft_num_frames(L, hop, center) == spec.shape[-1], (L, hop, center)
+    assert orc.stft_num_frames(2047, 441, False) == 0
 
 
 def test_rng_deterministic_and_normal(orc):
