@@ -643,6 +643,33 @@ def test_attention_bnhd_fusions(orc, dev, B, N, H, rot, gate, odt, tdt):
         assert_close(to_host(fused, odt), gref, odt, "attention_bnhd gate merge")
 
 
+@pytest.mark.parametrize("gdt,logit,odt", [(F32, True, BF16), (F16, True, F32), (BF16, False, BF16),
+                                           (F32, False, F32)])
+def test_attention_bnhd_gate_forms(orc, dev, gdt, logit, odt):
+    """The gated epilogue for every gate dtype, as logits or as probabilities, with a
+    non-default scale: bit for bit attention followed by the separate gate merge."""
+    say(f"attention_bnhd gate dtype={gdt} logit={logit} out={odt}")
+    B, N, H, scale = 2, 97, 3, 0.3
+    qkv = to_dev(inp(orc, (B, N, 3 * H * 64), 0x4D425200A5, N, BF16), BF16)
+    v5 = qkv.view(B, N, 3, H, 64)
+    q, k, v = v5[:, :, 0], v5[:, :, 1], v5[:, :, 2]
+    g_h = inp(orc, (B, N, H), 0x4D425200A6, N, gdt, std=2.0)
+    if not logit:   # probabilities in [0, 1]
+        g_h = orc.from_f32(np.abs(orc.to_f32(g_h, gdt)) / 6.0, gdt) if gdt != F32 else np.abs(g_h) / np.float32(6.0)
+    g = to_dev(g_h, gdt)
+    fused = mbrt.attention_bnhd(q, k, v, scale=scale, gate=g, gate_is_logit=logit,
+                                out_dtype=torch.float32 if odt == F32 else torch.bfloat16)
+    qc, kc, vc = (t.permute(0, 2, 1, 3).contiguous().view(B * H, N, 64) for t in (q, k, v))
+    att = empty((B, H, N, 64), odt)
+    mbrt.attention(qc, kc, vc, att.view(B * H, N, 64), scale)
+    sep = empty((B, N, H * 64), odt)
+    mbrt.gate_merge(att, g, sep, mbrt.LAYOUT_BHND, gate_is_logit=logit)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(fused, odt), to_host(sep, odt), "gated attention_bnhd = attention + gate merge")
+    gref = orc.gate_merge(to_host(att, odt), odt, g_h, gdt, odt, B, H, N, 64, layout=0, logit=logit)
+    assert_close(to_host(fused, odt), gref, odt, "gated attention_bnhd gate stage")
+
+
 def test_attention_bnhd_rejects_bad_strides(dev):
     t = torch.zeros((1, 16, 1, 68), dtype=torch.bfloat16, device="cuda")
     q = t[..., :64]  # rows 68 elements apart: not 16-byte pieces
