@@ -194,6 +194,9 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
         if (kt + kKeys < a.nk) load_tile(kt + kKeys, nbuf);
+        // a wave whose queries all lie past N (in the last query tile of a head) loads its
+        // share of every K/V tile and joins every barrier, but has nothing to compute
+        if (q0 >= a.nq) return;
 
         // S^T = K Q^T for the 4 key blocks of the tile and every query sub-block
         f32x4 st[QS][4];
