@@ -3,9 +3,9 @@
 Inputs are seeded (oracle RNG) and copied to the device; outputs come back through the
 C-ABI (mbrt ctypes binding) and are compared with the oracle on the same inputs under
 the rules in parity.py: bit-exact for copies, gathers and integer work; 1e-5 relative
-(f32) or 1 ulp + 2e-3 norm-wise (bf16/f16) for float math.  The BASELINE shapes run at
-full size where the oracle finishes in seconds, otherwise on a sampled set of rows plus
-size-independent properties over the whole tensor.
+(f32) or 1 ulp + 2e-3 norm-wise (bf16/f16) for float math.  The MelBandRoformer chunk
+shapes run at full size where the oracle finishes in seconds, otherwise on a sampled set
+of rows plus size-independent properties over the whole tensor.
 """
 from __future__ import annotations
 
