@@ -560,7 +560,10 @@ def test_zero_dc(orc, dev):
 # ---- fused attention -------------------------------------------------------------------------
 
 @pytest.mark.parametrize("BH,nq,nk", [(3, 1, 1), (3, 5, 5), (2, 60, 60), (2, 64, 64), (2, 65, 65), (2, 130, 130),
-                                      (2, 801, 801), (2, 37, 200), (2, 200, 37)])
+                                      (2, 801, 801), (2, 37, 200), (2, 200, 37),
+                                      # 128-query workgroups whose last one holds 1 or 33 queries (its
+                                      # other waves only load and sync), and one query or one key
+                                      (2, 129, 129), (1, 161, 70), (2, 1, 801), (2, 801, 1)])
 @pytest.mark.parametrize("odt", [BF16, F32])
 def test_attention_shapes(orc, dev, BH, nq, nk, odt):
     say(f"attention BH={BH} nq={nq} nk={nk} out={odt}")
