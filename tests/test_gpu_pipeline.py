@@ -94,3 +94,36 @@ def test_chunked_skeleton_reconstructs_a_song(orc, dev):
     rec = to_host(out, F32)[:, border:border + L]
     a = to_host(audio, F32)[0]
     assert np.abs(rec - a).max() <= 4e-6 * np.abs(a).max()
+
+
+def test_side_stream_matches_default_stream(orc, dev):
+    """Every call launches on the caller's current stream: the same ops on a second
+    (default-priority) stream give the same bits as on the default stream."""
+    say("softmax / attention / stft / istft / band chain on a side stream")
+    x = torch.from_numpy(orc.randn((300, 801), seed=0x4D425200A7, std=3.0)).to(dev)
+    q, k, v = (torch.from_numpy(orc.randn((8, 801, 64), seed=0x4D425200A8, stream=i)).to(dev).to(torch.bfloat16)
+               for i in range(3))
+    sig = torch.from_numpy(orc.randn((2, 2, 20000), seed=0x4D425200A9)).to(dev)
+    w = mbrt.hann_window(2048)
+    bands = _bands(dev)
+
+    def run():
+        y = torch.empty_like(x)
+        mbrt.softmax(x, y, 1.0)
+        o = torch.empty((8, 801, 64), dtype=torch.bfloat16, device=dev)
+        mbrt.attention(q, k, v, o, 0.0)
+        spec = mbrt.stft(sig.view(4, 20000), w, 441, True, False)
+        back = mbrt.istft(spec, w, 441, True, False, 20000)
+        return (y, o, spec, back, *_skeleton(sig, w, bands))
+
+    ref = run()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        got = run()
+    side.synchronize()
+    names = ("softmax", "attention", "stft", "istft", "chain stft", "chain merge", "chain istft")
+    assert len(ref) == len(names)
+    for name, a, b in zip(names, ref, got):
+        assert torch.equal(a, b), f"{name} differs on a side stream"
