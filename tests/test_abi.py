@@ -186,3 +186,30 @@ def test_chunk_fade_window_matches_oracle(lib, orc):
     null = C.c_void_p(0)
     assert lib.mbrt_chunk_fade_window(null, 10, 6, 0, 0) == 3   # fades overlap
 
+
+
+def test_last_error_is_per_thread(lib):
+    """Two threads making different bad calls each read back their own message (ctypes
+    drops the GIL around foreign calls, so the calls interleave)."""
+    import threading
+
+    null = C.c_void_p(0)
+    seen = {"glu": set(), "rotary": set()}
+
+    def glu():
+        for _ in range(3000):
+            assert lib.mbrt_glu_last_dim(null, 0, null, 0, 4, 0, null) == 3
+            seen["glu"].add(lib.mbrt_last_error().decode())
+
+    def rotary():
+        for _ in range(3000):
+            assert lib.mbrt_rotary_inplace(null, null, 3, null, null, 0, 5, 5, 1, 7, 0, null) == 3
+            seen["rotary"].add(lib.mbrt_last_error().decode())
+
+    threads = [threading.Thread(target=glu), threading.Thread(target=rotary)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert len(seen["glu"]) == 1 and len(seen["rotary"]) == 1
+    assert seen["glu"] != seen["rotary"] and all("even" in m for m in seen["rotary"])
