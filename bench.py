@@ -50,7 +50,11 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-threads", type=int, default=None)
+    ap.add_argument("--no-copy", action="store_true", help="skip the same-size copy timed beside every op")
+    ap.add_argument("--copy-ceiling", action="store_true",
+                    help="only measure the copy rate by size and the one-element launch time")
+    ap.add_argument("--cpu-threads", type=int, default=None,
+                    help="threads of the CPU baseline (default: the CPUs available, capped by OMP_NUM_THREADS)")
     ap.add_argument("--only", default=None,
                     help="comma-separated op-name substrings: time only those ops (tuning runs; "
                          "value then covers the selected ops only)")
@@ -69,6 +73,7 @@ class Op:
         self.run = None          # (buffer set) -> None
         self.ms = 0.0            # mean GPU time per call over the timed calls
         self.retimed = 0         # timings redone because the host enqueue outlasted the hold
+        self.copy_ms = 0.0       # a plain copy of the same bytes, timed the same way
 
 
 def build_ops(torch, mbrt, bands):
@@ -227,6 +232,96 @@ def build_ops(torch, mbrt, bands):
     return ops
 
 
+def make_sets(op):
+    """Enough buffer sets that the working set between two uses of one set exceeds the
+    MALL-defeat size, so that the 256 MB MALL cannot serve a repeat."""
+    first = op.make()
+    ws = sum(t.numel() * t.element_size() for t in first.values())
+    nsets = 1 if ws >= MALL_DEFEAT_BYTES else max(2, math.ceil(MALL_DEFEAT_BYTES / ws) + 1)
+    op.sets = [first] + [op.make() for _ in range(nsets - 1)]
+
+
+def make_timer(torch, stream, steps, warmup):
+    """Returns time_op(op): warm calls, then K back-to-back calls bracketed by one HIP event
+    pair on `stream`; op.ms = span / K.
+
+    The host enqueues the K calls while the stream is held by a spin kernel, so that they
+    run back to back on the GPU and the events time the kernels, not the Python launch path
+    (a ctypes call costs ~10 us, as long as the smaller ops).  Python's garbage collector is
+    off meanwhile, and should the enqueue still take more than half the hold, the op is
+    timed again with a longer hold: no GPU idle time can then fall inside the span."""
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(1 << 20)
+    c0.record(stream)
+    torch.cuda._sleep(1 << 20)
+    c1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_unit = max(c0.elapsed_time(c1), 1e-3)  # GPU ms of a 2^20-cycle spin
+
+    def time_op(op):
+        for i in range(warmup):
+            op.run(op.sets[i % len(op.sets)])
+        torch.cuda.synchronize()
+        hold_ms = 2.0 + 0.3 * steps
+        for attempt in range(4):
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            gc.disable()
+            try:
+                torch.cuda._sleep(int((1 << 20) * max(1.0, hold_ms / ms_per_unit)))
+                h0 = time.perf_counter()
+                a0.record(stream)
+                for i in range(steps):
+                    op.run(op.sets[(warmup + i) % len(op.sets)])
+                a1.record(stream)
+                enqueue_ms = (time.perf_counter() - h0) * 1e3
+            finally:
+                gc.enable()
+            torch.cuda.synchronize()
+            if enqueue_ms < 0.5 * hold_ms:
+                op.ms = a0.elapsed_time(a1) / steps
+                op.retimed = attempt
+                return
+            hold_ms *= 4
+        raise RuntimeError(f"bench.py: the host could not enqueue {op.name} within the stream hold")
+
+    return time_op
+
+
+def copy_op(torch, mbrt, nbytes):
+    """A plain contiguous copy that moves `nbytes` (half read, half written) with the
+    library's row-copy kernel: the ceiling an HBM-bound op of that size is compared with."""
+    n = max(4, int(nbytes) // 32 * 4)  # whole 16-byte vectors per buffer: the vector copy path
+    op = Op(f"copy_{nbytes}", n * 8, lambda: dict(x=torch.empty(n, device="cuda"), y=torch.empty(n, device="cuda")),
+            "row_copy_kernel")
+    op.run = lambda b: mbrt.strided_copy(b["x"], b["y"])
+    return op
+
+
+def copy_ceiling(torch, mbrt, args):
+    """--copy-ceiling: copy rate by size, and the time of a one-element launch (the fixed
+    cost every kernel pays between back-to-back calls on one stream)."""
+    stream = torch.cuda.current_stream()
+    time_op = make_timer(torch, stream, args.steps, args.warmup)
+    tiny = Op("launch_1_element", 8, lambda: dict(x=torch.empty(1, device="cuda")), "fill_kernel")
+    tiny.run = lambda b: mbrt.fill_(b["x"], 1.0)
+    tiny.sets = [tiny.make()]
+    time_op(tiny)
+    rows = []
+    for mb in (12.5, 25, 50, 75, 100, 150, 200, 300, 400, 600, 1000, 2000):
+        op = copy_op(torch, mbrt, int(mb * 1e6))
+        make_sets(op)
+        time_op(op)
+        rows.append({"bytes_moved": op.bytes, "us": round(op.ms * 1e3, 2),
+                     "gbs": round(op.bytes / (op.ms * 1e-3) / 1e9, 1)})
+        print(f"copy {op.bytes / 1e6:8.1f} MB moved: {op.ms * 1e3:8.2f} us  {rows[-1]['gbs']:7.1f} GB/s",
+              file=sys.stderr, flush=True)
+        op.sets = []
+        torch.cuda.empty_cache()
+    print(json.dumps({"copy_ceiling": rows, "launch_1_element_us": round(tiny.ms * 1e3, 3),
+                      "kernel": "row_copy_kernel<16, 2>", "steps": args.steps,
+                      "mall_defeat": f"buffer sets cycled past {MALL_DEFEAT_BYTES / 1e9:.1f} GB"}), flush=True)
+
+
 def band_tables(torch, mbrt):
     """60-band stereo layout (sr 44100, n_fft 2048) and its per-freq CSR, built on the
     host by the library (as the reference's loader does) and uploaded once."""
@@ -245,8 +340,33 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_threads_available() -> tuple[int, int]:
+    """(threads to use, CPUs visible to this process).  The threads are the CPUs this
+    process may run on, capped by OMP_NUM_THREADS when the host sets it: a shared host
+    gives each GPU a share of its cores and says so there."""
+    visible = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    use = min(visible, int(env)) if env.isdigit() and int(env) > 0 else visible
+    return use, visible
+
+
 def cpu_baseline(threads: int | None):
-    """Oracle float pipeline on a row sample of each op (OpenMP over rows)."""
+    """The oracle's float pipeline (f32 arithmetic, bf16 RNE on store, OpenMP over rows) on
+    a sample of every BL op, timed on this host: 1 warm run, then the median of 5 timed runs
+    per op, once on all the threads available and once on 1 thread."""
+    import statistics
+
     import numpy as np
 
     sys.path.insert(0, str(REPO / "oracle"))
@@ -254,10 +374,10 @@ def cpu_baseline(threads: int | None):
 
     if not O.LIB.exists():
         O.build()
-    nthreads = threads or min(16, os.cpu_count() or 1)
-    O.set_threads(nthreads)
+    use, visible = cpu_threads_available()
+    nthreads = threads or use
     rng = np.random.default_rng(0x4D42520000)
-    frac = 4  # 1/4 of the rows of every op, each timed over >= 1 s of repeats
+    frac = 2  # half of the rows (or frames) of every op
     rnd = lambda shape, std=1.0: (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
     bf = O.f32_to_bf16
     jobs = []
@@ -269,9 +389,10 @@ def cpu_baseline(threads: int | None):
     jobs.append(("bl2a", 2 * h.size * 2, lambda: O.bias_act(h, O.BF16, None, O.F32, O.BF16, 1, mode=O.FAST)))
     h2 = bf(rnd((48060 // frac, 3072), 1.5))
     jobs.append(("bl2b", h2.size * 2 * 3 // 2, lambda: O.glu(h2, O.BF16, O.BF16, mode=O.FAST)))
-    at, gl = bf(rnd((60 // 4, 8, 801, 64))), bf(rnd((60 // 4, 801, 8), 2.0))
+    nb = 60 // frac
+    at, gl = bf(rnd((nb, 8, 801, 64))), bf(rnd((nb, 801, 8), 2.0))
     jobs.append(("bl2c", 2 * at.size * 2 + gl.size * 2,
-                 lambda: O.gate_merge(at, O.BF16, gl, O.BF16, O.BF16, 15, 8, 801, 64, mode=O.FAST)))
+                 lambda: O.gate_merge(at, O.BF16, gl, O.BF16, O.BF16, nb, 8, 801, 64, mode=O.FAST)))
     for rows, cols in ((480 * 801 // frac, 801), (6408 * 60 // frac, 60)):
         s32 = rnd((rows, cols), 3.0)
         s16 = bf(s32)
@@ -280,13 +401,14 @@ def cpu_baseline(threads: int | None):
     q, k = bf(rnd((480 // frac, 801, 64))), bf(rnd((480 // frac, 801, 64)))
     cs, sn = O.rotary_tables(801, 64)
     jobs.append(("bl4a", 4 * q.size * 2, lambda: O.rotary(q, k, O.BF16, cs, sn, O.F32, 801, 1, mode=O.FAST)))
-    p = bf(rnd((4, 801, 60 // 4, 384)))
+    p = bf(rnd((4, 801, 60 // frac, 384)))
     pv = p.reshape(-1)
-    shp, strd = (4, 60 // 4, 801, 384), (801 * 15 * 384, 384, 15 * 384, 1)
+    fb = 60 // frac
+    shp, strd = (4, fb, 801, 384), (801 * fb * 384, 384, fb * 384, 1)
     jobs.append(("bl4b", 2 * p.size * 2, lambda: O.strided_copy(pv, shp, strd)))
     mb = O.mel_bands()
     J = mb["freq_indices"].size
-    T = 801 // 4
+    T = 801 // frac
     st = rnd((4, 2050, T, 2))
     jobs.append(("bl5a", st.size * 4 + 4 * T * J * 2 * 4, lambda: O.band_gather(st, mb["freq_indices"], O.F32, 4, 2050, T)))
     mk = rnd((4, T, J, 2), 0.5)
@@ -294,31 +416,42 @@ def cpu_baseline(threads: int | None):
     jobs.append(("bl5b", mk.size * 4 + 2 * st.size * 4,
                  lambda: O.band_mask_merge(st, [mk], O.F32, mb["csr_offsets"], mb["csr_indices"], cnt, O.F32, O.F32, 4,
                                            2050, T, 2, mode=O.FAST)))
-    tot_b, tot_t = 0, 0.0
-    per = {}
+
+    def run_all(n):
+        O.set_threads(n)
+        per, tot_s = {}, 0.0
+        for name, nbytes, fn in jobs:
+            fn()  # warm
+            ts = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            med = statistics.median(ts)
+            per[name] = round(nbytes / med / 1e9, 2)
+            tot_s += med
+        return per, tot_s
+
+    tot_b = sum(nb for _, nb, _ in jobs)
     wall0 = time.perf_counter()
-    for name, nb, fn in jobs:
-        fn()  # warm
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            fn()
-            reps += 1
-            t = time.perf_counter() - t0
-            if t >= 1.0 and reps >= 3:
-                break
-        per[name] = round(nb * reps / t / 1e9, 2)
-        tot_b += nb * reps
-        tot_t += t
+    per_all, s_all = run_all(nthreads)
+    per_one, s_one = run_all(1)
     wall = time.perf_counter() - wall0
     return {
-        "value": round(tot_b / tot_t / 1e9, 3),
+        "value": round(tot_b / s_all / 1e9, 3),
         "unit": "GB/s",
         "cores": nthreads,
         "kind": "port",
-        "sample": f"1/{frac} of the rows (or frames) of every BL-1..BL-5 op, oracle float pipeline "
-                  f"(oracle/oracle.cpp, ORC_FAST, OpenMP over rows), each op repeated for >= 1 s after a warm run; "
-                  f"{tot_b / 1e9:.2f} GB of algorithmic bytes in {tot_t:.1f} s of timed CPU work ({wall:.1f} s wall)",
-        "per_op_gbs": per,
+        "sample": f"1/{frac} of the rows (or frames) of every BL-1..BL-5 op ({tot_b / 1e9:.2f} GB of algorithmic "
+                  f"bytes per pass), oracle float pipeline (oracle/oracle.cpp, ORC_FAST, OpenMP static over rows, "
+                  f"-O3 -march=native); per op 1 warm run then the median of 5 timed runs; value = bytes / sum of "
+                  f"per-op medians on {nthreads} threads; {wall:.1f} s wall for both thread counts",
+        "cpu_model": cpu_model(),
+        "cpus_visible": visible,
+        "threads_available": use,
+        "threads_1_gbs": round(tot_b / s_one / 1e9, 3),
+        "per_op_gbs": per_all,
+        "per_op_gbs_1_thread": per_one,
     }
 
 
@@ -333,16 +466,16 @@ def main():
     import mbrt
 
     torch.cuda.set_device(0)
+    if args.copy_ceiling:
+        copy_ceiling(torch, mbrt, args)
+        return
     bands = band_tables(torch, mbrt)
     ops = build_ops(torch, mbrt, bands)
     if args.only:
         keys = [k for k in args.only.split(",") if k]
         ops = [op for op in ops if any(k in op.name for k in keys)]
     for op in ops:
-        first = op.make()
-        ws = sum(t.numel() * t.element_size() for t in first.values())
-        nsets = 1 if ws >= MALL_DEFEAT_BYTES else max(2, math.ceil(MALL_DEFEAT_BYTES / ws) + 1)
-        op.sets = [first] + [op.make() for _ in range(nsets - 1)]
+        make_sets(op)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
 
@@ -351,51 +484,22 @@ def main():
     # different op.  One HIP event pair on the kernels' stream brackets an op's K calls and
     # the op's time is that span over K: no events sit between the calls, as in a pipeline
     # (the reference's own benchmark reports time over N calls the same way).
-    #
-    # The host enqueues the K calls while the stream is held by a spin kernel, so that they
-    # run back to back on the GPU and the events time the kernels, not the Python launch path
-    # (a ctypes call costs ~10 us, as long as the smaller ops).  Python's garbage collector is
-    # off meanwhile, and should the enqueue still take more than half the hold, the op is
-    # timed again with a longer hold: no GPU idle time can then fall inside the span.
-    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(1 << 20)
-    c0.record(stream)
-    torch.cuda._sleep(1 << 20)
-    c1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_unit = max(c0.elapsed_time(c1), 1e-3)  # GPU ms of a 2^20-cycle spin
-
-    def time_op(op):
-        hold_ms = 2.0 + 0.3 * args.steps
-        for attempt in range(4):
-            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            gc.disable()
-            try:
-                torch.cuda._sleep(int((1 << 20) * max(1.0, hold_ms / ms_per_unit)))
-                h0 = time.perf_counter()
-                a0.record(stream)
-                for i in range(args.steps):
-                    op.run(op.sets[(args.warmup + i) % len(op.sets)])
-                a1.record(stream)
-                enqueue_ms = (time.perf_counter() - h0) * 1e3
-            finally:
-                gc.enable()
-            torch.cuda.synchronize()
-            if enqueue_ms < 0.5 * hold_ms:
-                op.ms = a0.elapsed_time(a1) / args.steps
-                op.retimed = attempt
-                return
-            hold_ms *= 4
-        raise RuntimeError(f"bench.py: the host could not enqueue {op.name} within the stream hold")
-
-    for op in ops:
-        for i in range(args.warmup):
-            op.run(op.sets[i % len(op.sets)])
-    torch.cuda.synchronize()
+    time_op = make_timer(torch, stream, args.steps, args.warmup)
     t0 = time.perf_counter()
     for op in ops:
         time_op(op)
     wall = time.perf_counter() - t0
+    # the ceiling each op is held against: a plain copy moving the same bytes, timed the same way
+    if not args.no_copy:
+        for op in ops:
+            if op.next:
+                continue
+            c = copy_op(torch, mbrt, op.bytes)
+            make_sets(c)
+            time_op(c)
+            op.copy_ms = c.ms
+            c.sets = []
+        torch.cuda.empty_cache()
 
     per_op = {}
     next_ops = {}
@@ -418,7 +522,11 @@ def main():
         gbs = op.bytes / (ms * 1e-3) / 1e9
         per_op[op.name] = {"bytes": op.bytes, "ms": round(ms, 5),
                            "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                           "dtype": op.name.rsplit("_", 1)[-1], "compute": "f32",
                            "buffer_sets": len(op.sets), "kernel": op.kernel}
+        if op.copy_ms:
+            per_op[op.name]["copy_same_bytes_gbs"] = round(op.bytes / (op.copy_ms * 1e-3) / 1e9, 1)
+            per_op[op.name]["frac_of_same_size_copy"] = round(op.copy_ms / ms, 4)
         if op.retimed:
             per_op[op.name]["retimed"] = op.retimed
         if gbs > HBM_PEAK_GBS:  # inputs are cycled past the MALL: this can only be a measurement error

@@ -1,6 +1,8 @@
 // Thread-local error state and generic entry points of the C-ABI.
 #include "abi_common.hpp"
 
+#include <atomic>
+
 namespace mbrt {
 
 static thread_local std::string t_error;
@@ -23,6 +25,18 @@ int check_launch(const char* op) {
         return set_error(MBRT_E_HIP, "%s: kernel launch failed: %s", op, hipGetErrorString(e));
     }
     return MBRT_OK;
+}
+
+int cu_count() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cached[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 }  // namespace mbrt

@@ -31,6 +31,9 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Kernel-launch epilogue: converts a launch failure into MBRT_E_HIP.
 int check_launch(const char* op);
 
+// Compute units of the current device (queried once per device), for persistent grids.
+int cu_count();
+
 // Largest grid.x we launch (2^31 - 1 allowed on AMD, but keep index math in 32 bits
 // where kernels assume it).
 constexpr int64_t kMaxGridX = 0x7fffffffLL;

@@ -197,6 +197,72 @@ __device__ __forceinline__ void fdivmod(uint32_t n, const FastDiv& f, uint32_t& 
     r = n - q * f.d;
 }
 
+// ---- direct-to-LDS loads and counted waits ---------------------------------------------
+// global_load_lds_*: lane i of a wave instruction writes its SIZE bytes at lds + SIZE * i
+// (lds is wave-uniform).  Such a load counts in vmcnt like any vector-memory instruction,
+// and on gfx9 vmcnt retires in issue order for loads and stores alike, so waiting until
+// at most N are outstanding completes everything issued before the last N.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void global_void;
+typedef __attribute__((address_space(4))) const int32_t const_i32;
+
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left free (gfx9 encoding: vmcnt in bits 3:0
+// and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// N ds_read_b64 at LDS byte address addr + OFF0 + i * STEP (i < N), completed before the
+// statement ends.  Written as one asm block so that the compiler neither sees these reads
+// (it would otherwise wait for every direct-to-LDS load in flight, vmcnt(0), before them:
+// it cannot tell one LDS buffer from another) nor touches the registers before the data
+// has arrived.  The caller orders them with its own vmcnt wait and barrier.
+template <int N, int OFF0, int STEP>
+__device__ __forceinline__ void lds_read_b64_n(uint32_t addr, f32x2 (&v)[N]) {
+    static_assert(N == 8 || N == 16, "8 or 16 reads");
+    static_assert(OFF0 >= 0 && OFF0 + (N - 1) * STEP < 65536, "ds offset is 16 bits");
+#define MBRT_DSR(i) "ds_read_b64 %" #i ", %[a] offset:%[o" #i "]\n\t"
+#define MBRT_OFF(i) [o##i] "n"(OFF0 + (i) * STEP)
+    if constexpr (N == 8) {
+        asm volatile(MBRT_DSR(0) MBRT_DSR(1) MBRT_DSR(2) MBRT_DSR(3) MBRT_DSR(4) MBRT_DSR(5) MBRT_DSR(6)
+                         MBRT_DSR(7) "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+                       "=&v"(v[7])
+                     : [a] "v"(addr), MBRT_OFF(0), MBRT_OFF(1), MBRT_OFF(2), MBRT_OFF(3), MBRT_OFF(4), MBRT_OFF(5),
+                       MBRT_OFF(6), MBRT_OFF(7)
+                     : "memory");
+    } else {
+        asm volatile(MBRT_DSR(0) MBRT_DSR(1) MBRT_DSR(2) MBRT_DSR(3) MBRT_DSR(4) MBRT_DSR(5) MBRT_DSR(6)
+                         MBRT_DSR(7) MBRT_DSR(8) MBRT_DSR(9) MBRT_DSR(10) MBRT_DSR(11) MBRT_DSR(12) MBRT_DSR(13)
+                             MBRT_DSR(14) MBRT_DSR(15) "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+                       "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]),
+                       "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15])
+                     : [a] "v"(addr), MBRT_OFF(0), MBRT_OFF(1), MBRT_OFF(2), MBRT_OFF(3), MBRT_OFF(4), MBRT_OFF(5),
+                       MBRT_OFF(6), MBRT_OFF(7), MBRT_OFF(8), MBRT_OFF(9), MBRT_OFF(10), MBRT_OFF(11),
+                       MBRT_OFF(12), MBRT_OFF(13), MBRT_OFF(14), MBRT_OFF(15)
+                     : "memory");
+    }
+#undef MBRT_DSR
+#undef MBRT_OFF
+}
+
+// LDS byte address of a __shared__ object.
+template <class T>
+__device__ __forceinline__ uint32_t lds_addr(const T* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p;
+}
+
+// A wave-uniform load through the scalar data cache (constant address space): the
+// address must be the same in every lane.  Used for small read-only tables (indices).
+__device__ __forceinline__ int32_t scalar_load_i32(const void* base, int64_t i) {
+    // global and constant address spaces share one 64-bit address on AMDGPU
+    const const_i32* p = (const const_i32*)(uintptr_t)base;
+    return p[i];
+}
+
 // MI355X deals the workgroups of a launch to its 8 XCDs round-robin (block p runs on XCD
 // p % 8), and each XCD has its own L2.  xcd_tile maps the linear block id p of an n-block
 // launch to a tile id so that every XCD walks one contiguous range of tile ids in order:

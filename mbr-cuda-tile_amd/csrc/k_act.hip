@@ -18,7 +18,9 @@ namespace mbrt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kU = MBRT_ACT_U;  // groups per thread
+constexpr int kU = MBRT_ACT_U;      // 16-byte groups per thread: bias + activation
+constexpr int kUGlu = MBRT_GLU_U;   // GLU
+constexpr int kUGate = MBRT_GATE_U; // sigmoid gate x head merge
 constexpr int kNoBias = -1;  // bias dtype tag: no bias
 
 __device__ __forceinline__ int64_t clamp_group(int64_t g, int64_t groups) { return g < groups ? g : groups - 1; }
@@ -115,10 +117,10 @@ struct GluArgs {
 template <int XDT, int ODT>
 __global__ __launch_bounds__(kThreads) void glu_vec_kernel(GluArgs a) {
     constexpr int VE = (XDT == F32 || ODT == F32) ? 4 : 8;
-    const int64_t base = (int64_t)blockIdx.x * (kThreads * kU) + threadIdx.x;
-    Vec<XDT, VE> xv[kU], gv[kU];
+    const int64_t base = (int64_t)blockIdx.x * (kThreads * kUGlu) + threadIdx.x;
+    Vec<XDT, VE> xv[kUGlu], gv[kUGlu];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kUGlu; ++u) {
         uint32_t row, c;
         fdivmod((uint32_t)clamp_group(base + u * kThreads, a.groups), a.gpr, row, c);
         const int64_t in0 = (int64_t)row * (2 * a.half) + (int64_t)c * VE;
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void glu_vec_kernel(GluArgs a) {
         gv[u].template load<MBRT_NT_GLU>(a.x, in0 + a.half);
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kUGlu; ++u) {
         const int64_t g = base + u * kThreads;
         if (g < a.groups) {
             float v[VE], gt[VE];
@@ -170,11 +172,11 @@ struct GateArgs {
 template <int ADT, int GDT, int ODT>
 __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
     constexpr int VE = (ADT == F32 || ODT == F32) ? 4 : 8;
-    const int64_t base = (int64_t)blockIdx.x * (kThreads * kU) + threadIdx.x;
-    Vec<ADT, VE> av[kU];
-    float gl[kU];
+    const int64_t base = (int64_t)blockIdx.x * (kThreads * kUGate) + threadIdx.x;
+    Vec<ADT, VE> av[kUGate];
+    float gl[kUGate];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kUGate; ++u) {
         const uint32_t g = (uint32_t)clamp_group(base + u * kThreads, a.groups);
         uint32_t token, rem, h, c;
         fdivmod(g, a.gpt, token, rem);
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
         gl[u] = ld1<GDT>(a.gate, (int64_t)token * a.H + h);
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kUGate; ++u) {
         const int64_t g = base + u * kThreads;
         if (g < a.groups) {
             float v[VE];
@@ -226,7 +228,9 @@ __global__ __launch_bounds__(kThreads) void gate_merge_elem_kernel(GateArgs a) {
 }
 
 inline dim3 elem_grid(int64_t n) { return dim3((unsigned)std::min<int64_t>(std::max<int64_t>(1, ceil_div(n, kThreads)), 1 << 20)); }
-inline dim3 vec_grid(int64_t groups) { return dim3((unsigned)std::max<int64_t>(1, ceil_div(groups, (int64_t)kThreads * kU))); }
+inline dim3 vec_grid(int64_t groups, int u = kU) {
+    return dim3((unsigned)std::max<int64_t>(1, ceil_div(groups, (int64_t)kThreads * u)));
+}
 
 }  // namespace
 }  // namespace mbrt
@@ -304,7 +308,7 @@ int mbrt_glu_last_dim(const void* x, int x_dtype, void* out, int out_dtype, int6
         with_dt(x_dtype, [&](auto xt) {
             with_dt(out_dtype, [&](auto ot) {
                 constexpr int X = decltype(xt)::value, O = decltype(ot)::value;
-                hipLaunchKernelGGL((glu_vec_kernel<X, O>), vec_grid(a.groups), dim3(kThreads), 0, st, a);
+                hipLaunchKernelGGL((glu_vec_kernel<X, O>), vec_grid(a.groups, kUGlu), dim3(kThreads), 0, st, a);
             });
         });
     } else {
@@ -351,7 +355,7 @@ int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const void* gate, 
             with_dt(gate_dtype, [&](auto gt) {
                 with_dt(out_dtype, [&](auto ot) {
                     constexpr int A = decltype(at)::value, G = decltype(gt)::value, O = decltype(ot)::value;
-                    hipLaunchKernelGGL((gate_merge_vec_kernel<A, G, O>), vec_grid(a.groups), dim3(kThreads), 0, st, a);
+                    hipLaunchKernelGGL((gate_merge_vec_kernel<A, G, O>), vec_grid(a.groups, kUGate), dim3(kThreads), 0, st, a);
                 });
             });
         });

@@ -49,8 +49,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;  // an LDS-resident bf16x4
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) const void global_void;
 
 // K/V tiles in LDS: [64 keys][64 d] bf16 without padding, a key row = eight 16-byte chunks.
 // Logical chunk j of key r sits at chunk j ^ (r & 7), so that the 16-byte fragment reads

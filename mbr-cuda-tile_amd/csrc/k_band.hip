@@ -10,9 +10,12 @@
 // so both stage 64-frame tiles through LDS: every global access is a run of consecutive
 // complex values along T (stft/out) or along J (bands), never a stride-T gather.
 //
-// Gather: a block owns (b, 64 frames, 64 band-bins).  It reads, for each band-bin j, the
-// 64 frames of stft row idx[j] (512 contiguous bytes), then writes, for each frame, the 64
-// band-bins (512 contiguous bytes of the output row).
+// Gather: a tile is (b, 64 frames, 64 band-bins).  For each band-bin j it reads the 64
+// frames of stft row idx[j] (512 contiguous bytes), then writes, for each frame, the 64
+// band-bins (512 contiguous bytes of the output row).  Persistent blocks walk the tiles
+// with three LDS buffers, so the rows of the next two tiles are in flight (direct-to-LDS
+// loads) while the current tile is stored; a one-tile-per-block kernel covers tensors
+// whose element offsets exceed 32 bits.  Indices outside [0, F) read the nearest row.
 //
 // Merge: a block owns (b, stem, 32 freqs, 64 frames).  The band-bins that feed those
 // freqs are the CSR entries [off[f0], off[f0+32]) (<= 64 when no freq has more than 2
@@ -118,6 +121,178 @@ __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
         const int tt = w + 4 * r;
         if (t0 + tt < a.T) store_complex<ODT>(a.out, (b * a.T + t0 + tt) * a.J + j, tile[lane][tt]);
     }
+}
+
+// ---- pipelined gather ----------------------------------------------------------------
+// Persistent blocks walk the tiles (band-bin tiles fastest, then frames, then batch) with a
+// stride of the grid size.  Three LDS buffers hold tiles i, i+1 and i+2: while tile i is
+// read out of LDS and stored, the stft rows of tiles i+1 and i+2 are in flight straight
+// into LDS (global_load_lds_dword: one wave instruction = 256 contiguous bytes = 32 frames
+// of one row), so no wave waits for a load it issued less than two tiles ago.
+//
+// Counting: per tile a wave issues a variable number of stores, then exactly kLPT direct
+// loads (row indices and frames are clamped, never skipped).  vmcnt retires in issue
+// order, so "at most kLPT outstanding" means every op before the newest tile's loads has
+// completed, in particular the loads of the tile about to be read.
+constexpr int kGTJ = 64;  // band-bins per tile: one per lane when storing
+
+struct GatherPipeArgs {
+    const float* stft;
+    const void* idx;
+    void* out;
+    int32_t F, T, J;
+    int32_t bft2;                 // F * T * 2: floats per batch of stft (B * F * T * 2 < 2^31)
+    FastDiv tiles_j, tiles_t;     // tile grid: band-bin tiles fastest, then frames, then batch
+    uint32_t tiles;
+};
+
+// Barrier for data that arrived by direct-to-LDS loads: the caller has waited (vmcnt) for
+// this wave's own loads; the barrier then makes every wave's data visible.  Unlike
+// __syncthreads() it carries no memory fence, which would wait for every outstanding
+// load, including those of the tiles still in flight.  The empty asm statements keep the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Freq of a row from its raw index (int32, or the low/high words of an int64), clamped
+// into [0, F): an index outside the tensor reads the nearest valid row.
+__device__ __forceinline__ int32_t clamp_freq(int32_t lo, int32_t hi, int32_t F) {
+    const int32_t f = hi == (lo >> 31) ? lo : (hi < 0 ? -1 : F);
+    return min(max(f, 0), F - 1);
+}
+
+template <int ODT, bool I64, int NW, int TT>
+__global__ __launch_bounds__(64 * NW) void band_gather_pipe_kernel(GatherPipeArgs a) {
+    constexpr int kRowF = 2 * TT + 2;    // floats per LDS row: TT complex values + 8 B of padding
+    constexpr int kRPW = kGTJ / NW;      // rows a wave loads per tile
+    constexpr int kIPR = TT / 32;        // direct loads per row
+    constexpr int kLPT = kRPW * kIPR;    // direct loads per wave per tile
+    constexpr int kFPW = TT / NW;        // frames a wave stores per tile
+    static_assert(TT % 32 == 0 && kGTJ % NW == 0 && TT % NW == 0 && kLPT < 64, "tile shape");
+    // three separate LDS objects: the compiler can tell the loads in flight into one buffer
+    // from the reads of another
+    __shared__ float buf0[kGTJ * kRowF];
+    __shared__ float buf1[kGTJ * kRowF];
+    __shared__ float buf2[kGTJ * kRowF];
+    const int lane = threadIdx.x % 64;
+    const int w = wave_id();
+    const int64_t n = a.tiles, G = gridDim.x;
+
+    struct Tile {
+        int32_t j0, t0, b;
+    };
+    // This block's tiles: blockIdx.x, + G, ..., dealt to the XCDs in runs of consecutive
+    // tiles.  (Giving each XCD its own range of band-bin columns, or walking the frame
+    // tiles of one column on one CU, cut the stft over-fetch but ran 15-20 % slower.)
+    const int64_t count = blockIdx.x < n ? (n - 1 - blockIdx.x) / G + 1 : 0;
+    auto tile = [&](int k) {
+        uint32_t tj, rest, tt, b;
+        fdivmod(xcd_runs<MBRT_BAND_XCD>((uint32_t)(blockIdx.x + (int64_t)k * G), a.tiles), a.tiles_j, rest, tj);
+        fdivmod(rest, a.tiles_t, b, tt);
+        return Tile{(int32_t)tj * kGTJ, (int32_t)tt * TT, (int32_t)b};
+    };
+    // raw indices of this wave's rows of a tile, by scalar loads (rows past J repeat row
+    // J - 1); they are clamped where used, so the loads of a tile are all in flight at once
+    int32_t flo[kRPW], fhi[kRPW];
+    auto fetch_rows = [&](const Tile& t) {
+        const int32_t jb = t.j0 + w * kRPW;
+#pragma unroll
+        for (int q = 0; q < kRPW; ++q) {
+            const int32_t j = min(jb + q, a.J - 1);
+            if constexpr (I64) {
+                flo[q] = scalar_load_i32(a.idx, 2 * (int64_t)j);
+                fhi[q] = scalar_load_i32(a.idx, 2 * (int64_t)j + 1);
+            } else {
+                flo[q] = scalar_load_i32(a.idx, j);
+            }
+        }
+    };
+    // lane l loads float (l & 1) of frame t0 + 32 h + l / 2 (clamped to the last frame)
+    auto issue = [&](const Tile& t, float* buf) {
+        int lo[kIPR];
+#pragma unroll
+        for (int h = 0; h < kIPR; ++h) lo[h] = min(t.t0 + 32 * h + lane / 2, a.T - 1) * 2 + (lane & 1);
+        // first LDS row of this wave, re-derived every step (kept out of registers across
+        // the loop: the rows of three buffers would not fit the scalar register file)
+        int32_t rb = w * kRPW;
+        asm volatile("" : "+s"(rb));
+#pragma unroll
+        for (int q = 0; q < kRPW; ++q) {
+            const int32_t f = clamp_freq(flo[q], I64 ? fhi[q] : (flo[q] >> 31), a.F);
+            const int32_t row = t.b * a.bft2 + f * a.T * 2;
+#pragma unroll
+            for (int h = 0; h < kIPR; ++h)
+                __builtin_amdgcn_global_load_lds((global_void*)(a.stft + row + lo[h]),
+                                                 (lds_void*)&buf[(rb + q) * kRowF + 64 * h], 4, 0, 0);
+        }
+    };
+    // lane = band-bin j0 + lane, frames w + NW r: one 8-byte LDS read and one store each
+    // (element offsets fit 32 bits: B * T * J * 2 < 2^31 is checked on the host)
+    auto store = [&](const Tile& t, const float* buf) {
+        f32x2 v[kFPW];
+        lds_read_b64_n<kFPW, 0, 8 * NW>(lds_addr(buf) + (uint32_t)(lane * kRowF + 2 * w) * 4, v);
+        const int32_t j = t.j0 + lane;
+        if (j >= a.J) return;
+        int32_t o = (t.b * a.T + t.t0 + w) * a.J + j;
+        const int32_t step_o = NW * a.J;
+        if (t.t0 + TT <= a.T) {
+#pragma unroll
+            for (int r = 0; r < kFPW; ++r, o += step_o) store_complex<ODT>(a.out, o, v[r]);
+        } else {
+            const int nv = (a.T - t.t0 - w + NW - 1) / NW;  // frames of this wave inside T
+#pragma unroll
+            for (int r = 0; r < kFPW; ++r, o += step_o)
+                if (r < nv) store_complex<ODT>(a.out, o, v[r]);
+        }
+    };
+    // Tile k of this block is p0 + k G and lives in buffer k % 3.  A steady step k reads
+    // tile k and issues the loads of tile k + 2 into the buffer that held tile k - 1; its
+    // issue order is the stores of tile k, then exactly kLPT loads, so at the next step
+    // only the newest kLPT ops may still be outstanding.  Every load of the steady loop is
+    // unconditional, which also lets the compiler's own wait before the LDS reads be the
+    // same vmcnt(kLPT).
+    if (count == 0) return;
+    const int m = (int)count;  // tiles of this block
+    auto steady = [&](int k, const float* cur, float* nxt2) {
+        wait_vmcnt<kLPT>();
+        // every wave's loads into `cur` have landed, and no wave still reads `nxt2`
+        lds_barrier();
+        store(tile(k), cur);
+        issue(tile(k + 2), nxt2);
+        if (k + 3 < m) fetch_rows(tile(k + 3));
+    };
+    fetch_rows(tile(0));
+    issue(tile(0), buf0);
+    if (m >= 2) {
+        fetch_rows(tile(1));
+        issue(tile(1), buf1);
+    }
+    int k = 0;
+    if (m >= 3) {
+        fetch_rows(tile(2));
+        for (;;) {
+            steady(k, buf0, buf2);
+            if (++k + 2 >= m) break;
+            steady(k, buf1, buf0);
+            if (++k + 2 >= m) break;
+            steady(k, buf2, buf1);
+            if (++k + 2 >= m) break;
+        }
+    }
+    // the last one or two tiles (k and k + 1), whose loads are already issued
+    auto buf_of = [&](int i) -> const float* { return i % 3 == 0 ? buf0 : i % 3 == 1 ? buf1 : buf2; };
+    if (k + 1 < m) {
+        wait_vmcnt<kLPT>();
+        lds_barrier();
+        store(tile(k), buf_of(k));
+        ++k;
+    }
+    wait_vmcnt<0>();
+    lds_barrier();
+    store(tile(k), buf_of(k));
 }
 
 struct MergeArgs {
@@ -266,6 +441,35 @@ int mbrt_band_gather(const float* stft, const void* freq_indices, int index_dtyp
     MBRT_REQUIRE(aligned(stft, 8) && aligned(out, out_dtype == F32 ? 8 : 4), MBRT_E_ALIGN,
                  "%s: complex buffers must be aligned to one complex value", op);
     GatherArgs a{stft, freq_indices, index_dtype == I64, out, out_dtype, total_freq, frames, n_band_freqs, 0, 0, 0};
+    if (MBRT_BAND_GATHER_PIPE && B * total_freq * frames * 2 < (int64_t(1) << 31) &&
+        B * frames * n_band_freqs * 2 < (int64_t(1) << 31)) {
+        constexpr int TT = MBRT_BAND_GTT, NW = MBRT_BAND_GNW;
+        GatherPipeArgs g{};
+        g.stft = stft;
+        g.idx = freq_indices;
+        g.out = out;
+        g.F = (int32_t)total_freq;
+        g.T = (int32_t)frames;
+        g.J = (int32_t)n_band_freqs;
+        g.bft2 = (int32_t)(total_freq * frames * 2);
+        const int64_t tj = ceil_div(n_band_freqs, kGTJ), tt = ceil_div(frames, TT), tiles = tj * tt * B;
+        g.tiles_j = make_fastdiv((uint32_t)tj);
+        g.tiles_t = make_fastdiv((uint32_t)tt);
+        g.tiles = (uint32_t)tiles;
+        // persistent grid: a multiple of the 8 XCDs, so that block b stays on XCD b % 8
+        int64_t grid = std::min<int64_t>(tiles, (int64_t)cu_count() * MBRT_BAND_GBPC);
+        if (grid >= kXcds) grid -= grid % kXcds;
+        with_dt(out_dtype, [&](auto ot) {
+            constexpr int O = decltype(ot)::value;
+            if (index_dtype == I64)
+                hipLaunchKernelGGL((band_gather_pipe_kernel<O, true, NW, TT>), dim3((unsigned)grid), dim3(64 * NW), 0,
+                                   as_stream(stream), g);
+            else
+                hipLaunchKernelGGL((band_gather_pipe_kernel<O, false, NW, TT>), dim3((unsigned)grid), dim3(64 * NW), 0,
+                                   as_stream(stream), g);
+        });
+        return check_launch(op);
+    }
     const int64_t tiles = ceil_div(n_band_freqs, kTJ) * ceil_div(frames, kTT) * B;
     MBRT_REQUIRE(tiles < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many tiles", op);
     a.tiles_j = (uint32_t)ceil_div(n_band_freqs, kTJ);

@@ -74,17 +74,18 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
     with_dt(a.odt, store_all);
 }
 
-// Staged short rows.  Block b owns rows [b*RB, b*RB + RB), RB = 256 / G, i.e. the span of
-// RB*cols elements starting at element b*RB*cols.  The launcher only picks this kernel when
+// Staged short rows.  Block b owns rows [b*RB, b*RB + RB), RB = RPG * 256 / G (each group
+// of G lanes takes RPG rows in turn), i.e. the span of RB*cols elements starting at element
+// b*RB*cols.  The launcher only picks this kernel when
 // that span is a whole number of 16-byte vectors for the input and the output dtype, both
 // pointers are 16-byte aligned and rows*cols fills whole vectors, so every vector lies in
 // one block's span.  Phase 1 loads the span (clamped vector indices, predicated LDS
 // writes), phase 2 is the same register-resident group softmax as above but fed from LDS,
 // writing the probabilities back over their inputs, phase 3 stores the span.  In-place
 // calls are safe: the whole span is in LDS before its first store.
-template <int IDT, int ODT, int G, int NM>
+template <int IDT, int ODT, int G, int NM, int RPG>
 __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
-    constexpr int RB = kThreads / G;
+    constexpr int RB = RPG * kThreads / G;
     constexpr int VI = 16 / DtSize<IDT>::value, VO = 16 / DtSize<ODT>::value;
     constexpr int CAP = RB * G * NM;  // floats of LDS (RB rows of at most G*NM elements)
     constexpr int KI = (CAP / VI + kThreads - 1) / kThreads, KO = (CAP / VO + kThreads - 1) / kThreads;
@@ -109,30 +110,34 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
         }
     }
     __syncthreads();
-    const int r = tid / G, lane = tid % G;
+    const int lane = tid % G;
     const int last = a.cols - 1;
-    const int rbase = min(r, nrows - 1) * a.cols;
-    float z[NM];
-    float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < NM; ++k) {
-        const float x = buf[rbase + min(lane + G * k, last)];
-        z[k] = lane + G * k <= last ? x * a.scale_log2e : -INFINITY;
-        m = fmaxf(m, z[k]);
-    }
-    m = group_max<G>(m);
-    float s = 0.0f;
+    for (int rr = 0; rr < RPG; ++rr) {
+        const int r = tid / G + rr * (kThreads / G);
+        const int rbase = min(r, nrows - 1) * a.cols;
+        float z[NM];
+        float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < NM; ++k) {
-        z[k] = __builtin_amdgcn_exp2f(z[k] - m);
-        s += z[k];
-    }
-    s = group_sum<G>(s);
-    const float inv = 1.0f / s;
-    if (r < nrows) {
+        for (int k = 0; k < NM; ++k) {
+            const float x = buf[rbase + min(lane + G * k, last)];
+            z[k] = lane + G * k <= last ? x * a.scale_log2e : -INFINITY;
+            m = fmaxf(m, z[k]);
+        }
+        m = group_max<G>(m);
+        float s = 0.0f;
 #pragma unroll
-        for (int k = 0; k < NM; ++k)
-            if (lane + G * k <= last) buf[rbase + lane + G * k] = z[k] * inv;
+        for (int k = 0; k < NM; ++k) {
+            z[k] = __builtin_amdgcn_exp2f(z[k] - m);
+            s += z[k];
+        }
+        s = group_sum<G>(s);
+        const float inv = 1.0f / s;
+        if (r < nrows) {
+#pragma unroll
+            for (int k = 0; k < NM; ++k)
+                if (lane + G * k <= last) buf[rbase + lane + G * k] = z[k] * inv;
+        }
     }
     __syncthreads();
     const int nvo = nel / VO;
@@ -169,11 +174,11 @@ __global__ __launch_bounds__(kThreads) void softmax_loop_kernel(SmArgs a, int id
                __builtin_amdgcn_exp2f(load1(a.in, idt, start + c) * a.scale_log2e - m) * inv);
 }
 
-template <int IDT, int G, int NM>
+template <int IDT, int G, int NM, int RPG = 1>
 void launch_staged(const SmArgs& a, hipStream_t st) {
     with_dt(a.odt, [&](auto ot) {
-        hipLaunchKernelGGL((softmax_staged_kernel<IDT, decltype(ot)::value, G, NM>),
-                           dim3((unsigned)ceil_div(a.rows, kThreads / G)), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((softmax_staged_kernel<IDT, decltype(ot)::value, G, NM, RPG>),
+                           dim3((unsigned)ceil_div(a.rows, RPG * kThreads / G)), dim3(kThreads), 0, st, a);
     });
 }
 
@@ -190,8 +195,12 @@ bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) 
             if (((int64_t)rb * c * es) % 16 != 0 || (a.rows * c * es) % 16 != 0) return false;
         return true;
     };
+    // rows of 33..64: a block of 32 rows moves 32*c*in_esize bytes in; below
+    // MBRT_SM_SHORT_BYTES of input its fixed cost dominates, so each group takes 2 rows
+    const bool two = 32 * c * in_esize < MBRT_SM_SHORT_BYTES;
     if (c <= 16 && fits(64)) launch_staged<IDT, 4, 4>(a, st);
     else if (c <= 32 && fits(32)) launch_staged<IDT, 8, 4>(a, st);
+    else if (c <= 64 && two && fits(64)) launch_staged<IDT, 8, 8, 2>(a, st);
     else if (c <= 64 && fits(32)) launch_staged<IDT, 8, 8>(a, st);
     else if (c <= 128 && fits(16)) launch_staged<IDT, 16, 8>(a, st);
     else if (c <= 128 || !MBRT_SM_STAGE_LONG) return false;

@@ -46,6 +46,18 @@
 #ifndef MBRT_BAND_XCD
 #define MBRT_BAND_XCD 8  // band kernels: runs of this many consecutive tiles per XCD (1: launch order)
 #endif
+#ifndef MBRT_BAND_GATHER_PIPE
+#define MBRT_BAND_GATHER_PIPE 1  // band gather: persistent pipelined blocks (1) or one tile per block (0)
+#endif
+#ifndef MBRT_BAND_GTT
+#define MBRT_BAND_GTT 64  // pipelined band gather: frames per tile (32 or 64)
+#endif
+#ifndef MBRT_BAND_GNW
+#define MBRT_BAND_GNW 4  // pipelined band gather: waves per block
+#endif
+#ifndef MBRT_BAND_GBPC
+#define MBRT_BAND_GBPC 1  // pipelined band gather: persistent blocks per CU
+#endif
 #ifndef MBRT_BAND_SLOAD
 #define MBRT_BAND_SLOAD 0  // band gather: row indices by scalar loads (1) or lane load + readlane (0)
 #endif
@@ -55,8 +67,17 @@
 #ifndef MBRT_SM_LONG_G
 #define MBRT_SM_LONG_G 64  // lanes per staged row of 129..1024 elements when 4-row spans align (64 or 32)
 #endif
+#ifndef MBRT_SM_SHORT_BYTES
+#define MBRT_SM_SHORT_BYTES 6144  // staged softmax rows of 33..64: below this many input bytes per 32 rows, 64-row blocks
+#endif
 #ifndef MBRT_ACT_U
-#define MBRT_ACT_U 1     // 16-byte groups per thread in the activation kernels
+#define MBRT_ACT_U 2     // 16-byte groups per thread: bias + activation (GELU)
+#endif
+#ifndef MBRT_GLU_U
+#define MBRT_GLU_U 1     // 16-byte output groups per thread: GLU
+#endif
+#ifndef MBRT_GATE_U
+#define MBRT_GATE_U 2    // 16-byte groups per thread: sigmoid gate x head merge
 #endif
 #ifndef MBRT_EW_U
 #define MBRT_EW_U 4      // 16-byte groups per thread in the elementwise kernels

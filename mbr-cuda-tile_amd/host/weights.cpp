@@ -437,15 +437,20 @@ ModelWeights ModelWeights::load(const std::string& path) {
         for (uint32_t d = 0; d < ndim; ++d) {
             e.shape[d] = file.i64();
             if (e.shape[d] < 0) throw std::runtime_error("ModelWeights: negative dimension for tensor " + e.name);
-            numel *= e.shape[d];
+            // a shape whose element count does not fit int64 cannot describe data in a file
+            if (__builtin_mul_overflow(numel, e.shape[d], &numel))
+                throw std::runtime_error("ModelWeights: tensor too large: " + e.name);
         }
         const uint32_t dt = file.u32();
         if (dt > 3)
             throw std::runtime_error("ModelWeights: unknown dtype " + std::to_string(dt) + " for tensor " + e.name);
         e.dtype = (DType)dt;
-        e.bytes = (size_t)numel * dtype_size(e.dtype);
+        int64_t nbytes = 0;
+        if (__builtin_mul_overflow(numel, (int64_t)dtype_size(e.dtype), &nbytes))
+            throw std::runtime_error("ModelWeights: tensor too large: " + e.name);
+        e.bytes = (size_t)nbytes;
         e.file_offset = file.tell();
-        if (e.file_offset + (int64_t)e.bytes > file_size)
+        if (nbytes > file_size - e.file_offset)
             throw std::runtime_error("ModelWeights: unexpected EOF reading data");
         file.seek(e.file_offset + (int64_t)e.bytes);
         e.arena_offset = arena;

@@ -629,13 +629,16 @@ int64_t orc_mel_bands(double sr, int n_fft, int n_bands, int C, int32_t* freq_in
 }
 
 // gather_freqs_fold_complex (src/mbr_cuda_tile.cu:4554-4601): out[b,t,j,c] = stft[b,idx[j],t,c].
+// An index outside [0, F) reads the nearest valid row (the library's contract; the
+// reference leaves such indices undefined).
 void orc_band_gather(const float* stft, const int32_t* idx, void* out, int odt, int64_t B, int64_t F, int64_t T,
                      int64_t J) {
 #pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t bt = 0; bt < B * T; ++bt) {
         const int64_t b = bt / T, t = bt % T;
         for (int64_t j = 0; j < J; ++j) {
-            const float* s = stft + ((b * F + idx[j]) * T + t) * 2;
+            const int64_t f = std::min<int64_t>(std::max<int64_t>(idx[j], 0), F - 1);
+            const float* s = stft + ((b * F + f) * T + t) * 2;
             const int64_t o = (bt * J + j) * 2;
             st(out, odt, o, s[0]);
             st(out, odt, o + 1, s[1]);

@@ -272,7 +272,8 @@ def mel_bands(sr=44100.0, n_fft=2048, n_bands=60, channels=2):
 
 
 def band_gather(stft, idx, odt, B, F, T):
-    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    # indices outside [0, F) read the nearest valid row; clip before narrowing to int32
+    idx = np.ascontiguousarray(np.clip(np.asarray(idx, dtype=np.int64), -1, F), dtype=np.int32)
     J = idx.size
     out = empty((B, T, J * 2), odt)
     lib().orc_band_gather(_p(stft), _p(idx), _p(out), odt, L(B), L(F), L(T), L(J))

@@ -186,11 +186,21 @@ def test_binary_bf16_is_f32_op_then_rne(orc):
 
 def test_broadcast_binary_matches_numpy(orc):
     a = orc.randn((3, 1, 5, 7), seed=15)
-    b = orc.randn((4, 1, 7), seed=16)
+    b = orc.randn((4, 1, 7), seed=16) + np.float32(3.0)
     out_shape = (3, 4, 5, 7)
     sa = [35, 0, 7, 1]
     sb = [0, 7, 0, 1]
-    assert_bitexact(orc.binary_broadcast(a, b, F32, out_shape, sa, sb, 0), a + b, "broadcast add")
+    for op, f in enumerate((np.add, np.subtract, np.multiply, np.divide)):
+        assert_bitexact(orc.binary_broadcast(a, b, F32, out_shape, sa, sb, op), f(a, b), f"broadcast op {op}")
+        # bf16: the f32 result of the widened operands, rounded once
+        ab, bb = orc.from_f32(a, BF16), orc.from_f32(b, BF16)
+        want = orc.from_f32(f(orc.bf16_to_f32(ab), orc.bf16_to_f32(bb)).astype(np.float32), BF16)
+        assert_bitexact(orc.binary_broadcast(ab, bb, BF16, out_shape, sa, sb, op), want, f"broadcast bf16 op {op}")
+    # a transposed (strided) operand
+    base = orc.randn((7, 5), seed=17)
+    c = orc.randn((3, 1, 7), seed=18)
+    assert_bitexact(orc.binary_broadcast(base, c, F32, (3, 5, 7), [0, 1, 5], [7, 0, 1], 1), base.T[None] - c,
+                    "broadcast strided")
 
 
 def test_strided_copy_permute_matches_numpy(orc):
@@ -385,6 +395,16 @@ def test_band_gather_matches_numpy(orc):
     got = orc.band_gather(stft, idx, F32, B, F, T)
     ref = stft[:, idx].transpose(0, 2, 1, 3).reshape(B, T, -1)
     assert_bitexact(got, np.ascontiguousarray(ref), "gather")
+
+
+def test_band_gather_clamps_out_of_range_indices(orc):
+    # an index outside [0, F) reads the nearest valid row: numpy's take(mode="clip")
+    B, F, T = 2, 50, 9
+    stft = orc.randn((B, F, T, 2), seed=53)
+    idx = np.array([0, -1, -7, 49, 50, 51, 10**6, -(2**40), 2**40, 3], dtype=np.int64)
+    got = orc.band_gather(stft, idx, F32, B, F, T)
+    ref = np.take(stft, idx, axis=1, mode="clip").transpose(0, 2, 1, 3).reshape(B, T, -1)
+    assert_bitexact(got, np.ascontiguousarray(ref), "gather clamp")
 
 
 def test_band_merge_kat_and_numpy(orc):
