@@ -167,15 +167,16 @@ def build_ops(torch, mbrt, bands):
     # Fused attention (MFMA), the first widening beyond the tensor-op path: q, k, v bf16
     # [BH, N, 64] for the time (480 x 801) and frequency (6408 x 60) attention.  Reported in
     # config.next_ops with TFLOP/s (4 BH N^2 64 flop); not part of `value`.
-    for atag, abh, an in (("time", 480, 801), ("freq", 6408, 60)):
-        op = Op(f"attention_{atag}_bf16", 4 * abh * an * 64 * 2,
+    for atag, abh, an, pb in (("time", 480, 801, False), ("freq", 6408, 60, False), ("time", 480, 801, True),
+                              ("freq", 6408, 60, True)):
+        op = Op(f"attention_{atag}_bf16" + ("_p_bf16" if pb else ""), 4 * abh * an * 64 * 2,
                 (lambda abh=abh, an=an: dict(q=randn((abh, an, 64), bf16), k=randn((abh, an, 64), bf16),
                                              v=randn((abh, an, 64), bf16),
                                              y=torch.empty((abh, an, 64), dtype=bf16, device=dev))),
                 "attention_kernel")
         op.flops = 4.0 * abh * an * an * 64
         op.next = True
-        op.run = lambda b: mbrt.attention(b["q"], b["k"], b["v"], b["y"], 0.125)
+        op.run = lambda b, pb=pb: mbrt.attention(b["q"], b["k"], b["v"], b["y"], 0.125, p_bf16=pb)
         ops.append(op)
     # The time attention as the reference's split-contig q-rotary form plus the gate: q, k, v
     # read in place from the fused qkv projection [60, 801, 3*8*64], q rotated in the kernel,
@@ -510,9 +511,13 @@ def main():
         gbs = op.bytes / (ms * 1e-3) / 1e9
         if op.flops > 0:
             tf = op.flops / (ms * 1e-3) / 1e12
+            # the roof that bounds it: MFMA above the ridge point (peak flop/s over peak B/s)
+            mfma = op.flops / op.bytes > MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
             next_ops[op.name] = {"flops": op.flops, "bytes": op.bytes, "ms": round(ms, 5), "tflops": round(tf, 1),
                                  "frac_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                                 "gbs": round(gbs, 1), "kernel": op.kernel}
+                                 "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                 "flop_per_byte": round(op.flops / op.bytes, 1), "bound": "mfma" if mfma else "hbm",
+                                 "kernel": op.kernel}
         else:
             next_ops[op.name] = {"bytes": op.bytes, "ms": round(ms, 5), "gbs": round(gbs, 1),
                                  "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "kernel": op.kernel}

@@ -351,6 +351,27 @@ MBRT_API int mbrt_attention_strided(const void* q, const void* k, const void* v,
                                     int gate_is_logit, void* out, int out_dtype, float scale,
                                     mbrt_stream_t stream);
 
+/* Precision of the probabilities P in the attention's second product (O = P V). */
+enum mbrt_attn_precision {
+    MBRT_ATTN_P_PAIR = 0, /* P as a bf16 hi + lo pair: f32 accuracy (mbrt_attention's default) */
+    MBRT_ATTN_P_BF16 = 1  /* the reference's arithmetic: running max per 64-key tile, P
+                             rounded once to bf16 for one P V product, the row sum over
+                             the unrounded P (src/mbr_time_attention_cutile.cu:160-180) */
+};
+
+/* mbrt_attention_strided with the P precision chosen (enum mbrt_attn_precision).
+ * MBRT_ATTN_P_BF16 runs one MFMA per key tile instead of two and matches the
+ * reference's rounding of P; its output differs from exact attention by ~1e-3 of the
+ * output's RMS (one bf16 rounding of every P).  Replaces the same reference functions
+ * as mbrt_attention_strided. */
+MBRT_API int mbrt_attention_ex(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                               int64_t n_q, int64_t n_k, int64_t head_dim, int64_t q_batch_stride,
+                               int64_t q_head_stride, int64_t q_row_stride, int64_t kv_batch_stride,
+                               int64_t kv_head_stride, int64_t kv_row_stride, const void* rot_cos,
+                               const void* rot_sin, int trig_dtype, const void* gate, int gate_dtype,
+                               int gate_is_logit, void* out, int out_dtype, float scale, int p_precision,
+                               mbrt_stream_t stream);
+
 /* ---- STFT / iSTFT (n_fft = win_length = 2048) --------------------------------- */
 
 /* Hann window of `size` f32 samples, 0.5 (1 - cos(2 pi n / size)) in f32; size 1 gives

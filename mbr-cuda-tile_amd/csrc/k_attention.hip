@@ -89,7 +89,11 @@ __device__ __forceinline__ float xor_sum(float x) {
 
 // QS = 16-query sub-blocks per wave (1 or 2): every K and V^T fragment read from LDS
 // feeds QS MFMAs, so longer sequences use QS = 2 (128 queries per workgroup).
-template <int ODT, int QS>
+// PM = precision of P in the second product: MBRT_ATTN_P_PAIR (P as a bf16 hi + lo pair,
+// f32 accuracy, lazy max) or MBRT_ATTN_P_BF16 (the reference's arithmetic,
+// src/mbr_time_attention_cutile.cu:160-180: the running max moves every 64-key tile, P is
+// rounded once to bf16 for one P V product, and the row sum adds the unrounded P).
+template <int ODT, int QS, int PM>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
     // two K and two V tiles: the next pair is loaded (straight into LDS) while the current
     // one is read
@@ -221,6 +225,32 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
                     for (int i = 0; i < 4; ++i)
                         if (kt + 16 * kb + 4 * g + i >= a.nk) st[x][kb][i] = -INFINITY;
         }
+        if constexpr (PM == MBRT_ATTN_P_BF16 && !MBRT_ATTN_PBF16_LAZY) {
+            // the reference's running max: m[x] = max(m[x], max of the tile's scaled scores)
+            // every tile, the accumulator and row sum rescaled by exp2(m_old - m_new)
+#pragma unroll
+            for (int x = 0; x < QS; ++x) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+                    mx = fmaxf(mx, fmaxf(fmaxf(st[x][kb][0], st[x][kb][1]), fmaxf(st[x][kb][2], st[x][kb][3])));
+                const float mn = fmaxf(m[x], xor_max(mx) * a.scale_log2e);
+                const float alpha = __builtin_amdgcn_exp2f(m[x] - mn);
+                l[x] *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) o[x][db] *= alpha;
+                m[x] = mn;
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float p = __builtin_amdgcn_exp2f(fmaf(st[x][kb][i], a.scale_log2e, -m[x]));
+                        st[x][kb][i] = p;
+                        l[x] += p;
+                    }
+                }
+            }
+        } else {
 #pragma unroll
         for (int x = 0; x < QS; ++x) {
             // m[x] is the exponent reference in log2 units, the same in the four lanes of a
@@ -256,6 +286,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
             }
         }
 
+        }  // PM
         // O^T += V^T P^T over the two 32-key chunks.  P = P_hi + P_lo, both bf16: hi is P
         // truncated to bf16 (exact), lo = P - hi (exact in f32) rounded to bf16, so the
         // pair carries 16 mantissa bits and the product keeps f32 accuracy.
@@ -270,14 +301,18 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
                     for (int i = 0; i < 4; i += 2) {
                         const float p0 = st[x][2 * cc + h][i], p1 = st[x][2 * cc + h][i + 1];
-                        const uint32_t b0 = __float_as_uint(p0) & 0xffff0000u;
-                        const uint32_t b1 = __float_as_uint(p1) & 0xffff0000u;
-                        hw[2 * h + i / 2] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
-                        lw[2 * h + i / 2] = pack_bf16x2(p0 - __uint_as_float(b0), p1 - __uint_as_float(b1));
+                        if constexpr (PM == MBRT_ATTN_P_BF16) {
+                            hw[2 * h + i / 2] = pack_bf16x2(p0, p1);  // one RNE rounding
+                        } else {
+                            const uint32_t b0 = __float_as_uint(p0) & 0xffff0000u;
+                            const uint32_t b1 = __float_as_uint(p1) & 0xffff0000u;
+                            hw[2 * h + i / 2] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+                            lw[2 * h + i / 2] = pack_bf16x2(p0 - __uint_as_float(b0), p1 - __uint_as_float(b1));
+                        }
                     }
                 }
                 ph[x] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
-                pl[x] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+                if constexpr (PM != MBRT_ATTN_P_BF16) pl[x] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
             }
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
@@ -292,7 +327,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
                 for (int x = 0; x < QS; ++x) {
                     o[x][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[x], o[x][db], 0, 0, 0);
-                    o[x][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[x], o[x][db], 0, 0, 0);
+                    if constexpr (PM != MBRT_ATTN_P_BF16)
+                        o[x][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[x], o[x][db], 0, 0, 0);
                 }
             }
         }
@@ -354,13 +390,15 @@ using namespace mbrt;
 
 extern "C" {
 
-int mbrt_attention_strided(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t n_q,
-                           int64_t n_k, int64_t head_dim, int64_t q_batch_stride, int64_t q_head_stride,
-                           int64_t q_row_stride, int64_t kv_batch_stride, int64_t kv_head_stride,
-                           int64_t kv_row_stride, const void* rot_cos, const void* rot_sin, int trig_dtype,
-                           const void* gate, int gate_dtype, int gate_is_logit, void* out, int out_dtype,
-                           float scale, mbrt_stream_t stream) {
+int mbrt_attention_ex(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t n_q,
+                      int64_t n_k, int64_t head_dim, int64_t q_batch_stride, int64_t q_head_stride,
+                      int64_t q_row_stride, int64_t kv_batch_stride, int64_t kv_head_stride, int64_t kv_row_stride,
+                      const void* rot_cos, const void* rot_sin, int trig_dtype, const void* gate, int gate_dtype,
+                      int gate_is_logit, void* out, int out_dtype, float scale, int p_precision,
+                      mbrt_stream_t stream) {
     const char* op = "mbrt_attention";
+    MBRT_REQUIRE(p_precision == MBRT_ATTN_P_PAIR || p_precision == MBRT_ATTN_P_BF16, MBRT_E_INVALID_ARG,
+                 "%s: unknown P precision %d", op, p_precision);
     MBRT_REQUIRE(dtype == BF16, MBRT_E_UNSUPPORTED_DTYPE, "%s: q/k/v must be BF16", op);
     MBRT_REQUIRE(out_dtype == BF16 || out_dtype == F32, MBRT_E_UNSUPPORTED_DTYPE, "%s: out must be BF16/F32", op);
     MBRT_REQUIRE(head_dim == kHeadDim, MBRT_E_SHAPE, "%s: head_dim %lld (only 64 is built)", op, (long long)head_dim);
@@ -422,14 +460,30 @@ int mbrt_attention_strided(const void* q, const void* k, const void* v, int dtyp
     MBRT_REQUIRE(BH * a.qtiles < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many tiles", op);
     const dim3 grid((unsigned)(BH * a.qtiles));
     hipStream_t stm = as_stream(stream);
-    if (qs == 2) {
-        if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 2>), grid, dim3(kWaves * 64), 0, stm, a);
-        else hipLaunchKernelGGL((attention_kernel<F32, 2>), grid, dim3(kWaves * 64), 0, stm, a);
-    } else {
-        if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 1>), grid, dim3(kWaves * 64), 0, stm, a);
-        else hipLaunchKernelGGL((attention_kernel<F32, 1>), grid, dim3(kWaves * 64), 0, stm, a);
-    }
+    auto launch = [&](auto pm) {
+        constexpr int PM = decltype(pm)::value;
+        if (qs == 2) {
+            if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 2, PM>), grid, dim3(kWaves * 64), 0, stm, a);
+            else hipLaunchKernelGGL((attention_kernel<F32, 2, PM>), grid, dim3(kWaves * 64), 0, stm, a);
+        } else {
+            if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 1, PM>), grid, dim3(kWaves * 64), 0, stm, a);
+            else hipLaunchKernelGGL((attention_kernel<F32, 1, PM>), grid, dim3(kWaves * 64), 0, stm, a);
+        }
+    };
+    if (p_precision == MBRT_ATTN_P_BF16) launch(std::integral_constant<int, MBRT_ATTN_P_BF16>{});
+    else launch(std::integral_constant<int, MBRT_ATTN_P_PAIR>{});
     return check_launch(op);
+}
+
+int mbrt_attention_strided(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t n_q,
+                           int64_t n_k, int64_t head_dim, int64_t q_batch_stride, int64_t q_head_stride,
+                           int64_t q_row_stride, int64_t kv_batch_stride, int64_t kv_head_stride,
+                           int64_t kv_row_stride, const void* rot_cos, const void* rot_sin, int trig_dtype,
+                           const void* gate, int gate_dtype, int gate_is_logit, void* out, int out_dtype,
+                           float scale, mbrt_stream_t stream) {
+    return mbrt_attention_ex(q, k, v, dtype, B, H, n_q, n_k, head_dim, q_batch_stride, q_head_stride, q_row_stride,
+                             kv_batch_stride, kv_head_stride, kv_row_stride, rot_cos, rot_sin, trig_dtype, gate,
+                             gate_dtype, gate_is_logit, out, out_dtype, scale, MBRT_ATTN_P_PAIR, stream);
 }
 
 int mbrt_attention(const void* q, const void* k, const void* v, int dtype, void* out, int out_dtype, int64_t BH,

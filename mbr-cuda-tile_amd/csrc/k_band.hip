@@ -321,10 +321,21 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     // one linear grid; neighbouring freq tiles (whose CSR runs split cache lines of the
     // mask rows) run on one XCD
     const uint32_t tile = xcd_runs<MBRT_BAND_XCD>(blockIdx.x, a.tiles);
-    const uint32_t tf = tile % a.tiles_f, rest = tile / a.tiles_f;
+    uint32_t tf, tt, rest;
+    if constexpr (MBRT_BAND_MERGE_TFAST) {
+        tt = tile % a.tiles_t;
+        rest = tile / a.tiles_t;
+        tf = rest % a.tiles_f;
+        rest = rest / a.tiles_f;
+    } else {
+        tf = tile % a.tiles_f;
+        rest = tile / a.tiles_f;
+        tt = rest % a.tiles_t;
+        rest = rest / a.tiles_t;
+    }
     const int f0 = (int)tf * kTF;
-    const int t0 = (int)(rest % a.tiles_t) * kTT;
-    const int bs = (int)(rest / a.tiles_t);  // b * S + s
+    const int t0 = (int)tt * kTT;
+    const int bs = (int)rest;  // b * S + s
     const int b = a.S == 2 ? bs >> 1 : bs;
     const void* mask = a.mask[bs - b * a.S];
     const int lane = threadIdx.x % 64;

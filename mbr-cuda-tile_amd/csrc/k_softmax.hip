@@ -196,11 +196,12 @@ bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) 
         return true;
     };
     // rows of 33..64: a block of 32 rows moves 32*c*in_esize bytes in; below
-    // MBRT_SM_SHORT_BYTES of input its fixed cost dominates, so each group takes 2 rows
+    // MBRT_SM_SHORT_BYTES of input its fixed cost dominates, so each group takes
+    // MBRT_SM_SHORT_RPG rows
     const bool two = 32 * c * in_esize < MBRT_SM_SHORT_BYTES;
     if (c <= 16 && fits(64)) launch_staged<IDT, 4, 4>(a, st);
     else if (c <= 32 && fits(32)) launch_staged<IDT, 8, 4>(a, st);
-    else if (c <= 64 && two && fits(64)) launch_staged<IDT, 8, 8, 2>(a, st);
+    else if (c <= 64 && two && fits(32 * MBRT_SM_SHORT_RPG)) launch_staged<IDT, 8, 8, MBRT_SM_SHORT_RPG>(a, st);
     else if (c <= 64 && fits(32)) launch_staged<IDT, 8, 8>(a, st);
     else if (c <= 128 && fits(16)) launch_staged<IDT, 16, 8>(a, st);
     else if (c <= 128 || !MBRT_SM_STAGE_LONG) return false;

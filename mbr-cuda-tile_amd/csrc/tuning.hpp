@@ -58,6 +58,9 @@
 #ifndef MBRT_BAND_GBPC
 #define MBRT_BAND_GBPC 1  // pipelined band gather: persistent blocks per CU
 #endif
+#ifndef MBRT_BAND_MERGE_TFAST
+#define MBRT_BAND_MERGE_TFAST 0  // band merge tile order: frame tiles fastest (1) or freq tiles fastest (0)
+#endif
 #ifndef MBRT_BAND_SLOAD
 #define MBRT_BAND_SLOAD 0  // band gather: row indices by scalar loads (1) or lane load + readlane (0)
 #endif
@@ -69,6 +72,12 @@
 #endif
 #ifndef MBRT_SM_SHORT_BYTES
 #define MBRT_SM_SHORT_BYTES 6144  // staged softmax rows of 33..64: below this many input bytes per 32 rows, 64-row blocks
+#endif
+#ifndef MBRT_SM_SHORT_RPG
+#define MBRT_SM_SHORT_RPG 2  // rows per lane group in those blocks
+#endif
+#ifndef MBRT_ATTN_PBF16_LAZY
+#define MBRT_ATTN_PBF16_LAZY 0  // P-bf16 attention: the lazy running max of the pair mode (1) instead of the reference's per-tile max (0)
 #endif
 #ifndef MBRT_ACT_U
 #define MBRT_ACT_U 2     // 16-byte groups per thread: bias + activation (GELU)

@@ -97,6 +97,7 @@ SIGNATURES: dict[str, list] = {
     "mbrt_zero_dc": [P, I, L, L, L, P],
     "mbrt_attention": [P, P, P, I, P, I, L, L, L, L, Fl, P],
     "mbrt_attention_strided": [P, P, P, I, L, L, L, L, L, L, L, L, L, L, L, P, P, I, P, I, I, P, I, Fl, P],
+    "mbrt_attention_ex": [P, P, P, I, L, L, L, L, L, L, L, L, L, L, L, P, P, I, P, I, I, P, I, Fl, I, P],
     "mbrt_hann_window": [P, L, P],
     "mbrt_stft_num_frames": [L, L, I],
     "mbrt_stft": [P, P, P, L, L, L, L, L, L, I, I, P],

@@ -740,4 +740,45 @@ void orc_attention(const void* q, const void* k, const void* v, int dt, void* ou
     }
 }
 
+// The reference's arithmetic of P in the time attention (src/mbr_time_attention_cutile.cu:
+// 160-180), in double: keys in tiles of 64 (one of its KTile choices); the running max
+// m moves to the max of each tile's scaled scores; P = exp(s - m) is rounded once to bf16
+// for the P V sum while the row sum l adds the unrounded P; both are rescaled by
+// exp(m_old - m_new); out = O / l rounded once to odt.
+void orc_attention_ref_p(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
+                         int64_t nq, int64_t nk, int64_t D, float scale) {
+    const double sc = scale == 0.0f ? 1.0 / std::sqrt((double)D) : (double)scale;
+    const int64_t kTile = 64;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int64_t r = 0; r < BH * nq; ++r) {
+        const int64_t bh = r / nq;
+        const int64_t qb = r * D, kb0 = bh * nk * D;
+        std::vector<double> s((size_t)kTile), o((size_t)D, 0.0);
+        double m = -INFINITY, l = 0.0;
+        for (int64_t k0 = 0; k0 < nk; k0 += kTile) {
+            const int64_t n = std::min(kTile, nk - k0);
+            double tm = -INFINITY;
+            for (int64_t j = 0; j < n; ++j) {
+                double acc = 0.0;
+                for (int64_t d = 0; d < D; ++d)
+                    acc += (double)ld(q, dt, qb + d) * (double)ld(k, dt, kb0 + (k0 + j) * D + d);
+                s[j] = acc * sc;
+                tm = std::max(tm, s[j]);
+            }
+            const double mn = std::max(m, tm);
+            const double alpha = std::exp(m - mn);
+            l *= alpha;
+            for (int64_t d = 0; d < D; ++d) o[d] *= alpha;
+            m = mn;
+            for (int64_t j = 0; j < n; ++j) {
+                const double p = std::exp(s[j] - m);
+                l += p;
+                const double pb = (double)bf16_to_f32(f64_to_bf16(p));
+                for (int64_t d = 0; d < D; ++d) o[d] += pb * (double)ld(v, dt, kb0 + (k0 + j) * D + d);
+            }
+        }
+        for (int64_t d = 0; d < D; ++d) st(out, odt, r * D + d, o[d] / l);
+    }
+}
+
 }  // extern "C"

@@ -88,6 +88,9 @@ void orc_band_mask_merge(const float* stft, const void* const* masks, int mdt, i
 void orc_zero_dc(void* spec, int dt, int64_t outer, int64_t bins, int64_t T);
 void orc_attention(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
                    int64_t nq, int64_t nk, int64_t D, float scale, int mode);
+/* the time attention with the reference's rounding of P (src/mbr_time_attention_cutile.cu:160-180) */
+void orc_attention_ref_p(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
+                         int64_t nq, int64_t nk, int64_t D, float scale);
 
 #ifdef __cplusplus
 }

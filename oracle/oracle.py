@@ -308,6 +308,16 @@ def attention(q, k, v, dt, odt, scale=0.0, mode=EXACT):
     return out
 
 
+def attention_ref_p(q, k, v, dt, odt, scale=0.0):
+    """The attention with the reference's P arithmetic: running max per 64-key tile, P
+    rounded once to bf16 for P V, row sum over the unrounded P (double elsewhere)."""
+    BH, nq, D = q.shape
+    nk = k.shape[1]
+    out = empty((BH, nq, D), odt)
+    lib().orc_attention_ref_p(_p(q), _p(k), _p(v), dt, _p(out), odt, L(BH), L(nq), L(nk), L(D), C.c_float(scale))
+    return out
+
+
 # ---- STFT / iSTFT, n_fft = win_length = 2048 (src/stft_cuda_tile.cu) ----------------------
 # Restated in numpy float64: the frame DFT is evaluated with numpy's FFT (an exact-maths
 # evaluator, pinned in tests against a direct O(N^2) DFT and torch.stft / torch.istft).

@@ -668,6 +668,89 @@ def test_attention_shapes(orc, dev, BH, nq, nk, odt):
     print("attention errors", assert_close(to_host(out, odt), ref, odt, "attention", den=den))
 
 
+def _pmax_v(q, k, v, scale):
+    """max_j p_ij |v_jd| for every (query i, d), p the exact softmax (double): the size of
+    the largest single term of an output, i.e. what one bf16 step of one P moves it by
+    / 2^-8."""
+    qd, kd, vd = (np.asarray(t, np.float64) for t in (q, k, v))
+    s = np.einsum("bid,bjd->bij", qd, kd) * (scale or 1.0 / 8.0)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return np.max(p[..., :, None] * np.abs(vd)[:, None, :, :], axis=2)
+
+
+def _assert_ref_p(orc, y, q, k, v, odt, scale, what):
+    """The reference-P attention against the oracle variant that restates its rounding.  The
+    kernel's P (f32 exp2) and the oracle's (double exp) round to different bf16 neighbours
+    only within a few f32 ulps of a rounding boundary; each such flip moves an output by at
+    most 2^-8 of its largest term, so the elementwise bound is 2^-7 max_j p|v| (two flips)
+    plus the f32 rule on sum p|v| (plus 1 ulp for bf16 outputs); norm-wise it is 2e-4
+    (2e-3 for bf16 outputs, the usual rule).  Against exact attention it is within one
+    bf16 rounding of every P: norm-wise 2^-8."""
+    qf, kf, vf = (orc.to_f32(t, BF16) for t in (q, k, v))
+    ref = orc.attention_ref_p(q, k, v, BF16, odt, scale)
+    den = orc.attention(qf, kf, np.abs(vf), F32, F32, scale).astype(np.float64)
+    pm = _pmax_v(qf, kf, vf, scale)
+    a, b = orc.to_f32(y, odt).astype(np.float64), orc.to_f32(ref, odt).astype(np.float64)
+    bound = 2.0 ** -7 * pm + 1e-5 * den
+    if odt == BF16:
+        bound = bound + 2.0 ** (np.floor(np.log2(np.maximum(np.abs(b), 1e-30))) - 7)
+    excess = np.abs(a - b) - bound
+    worst = np.unravel_index(np.argmax(excess), excess.shape)
+    assert excess[worst] <= 0, f"{what}: {a[worst]} vs {b[worst]} (bound {bound[worst]:.3e})"
+    norm = np.linalg.norm(a - b) / np.linalg.norm(b)
+    assert norm <= (2e-3 if odt == BF16 else 2e-4), f"{what}: norm-wise {norm:.3e}"
+    exact = orc.attention(q, k, v, BF16, F32, scale).astype(np.float64)
+    assert np.linalg.norm(a - exact) / np.linalg.norm(exact) <= 2.0 ** -8, f"{what}: vs exact attention"
+    return norm
+
+
+@pytest.mark.parametrize("BH,nq,nk", [(3, 1, 1), (2, 65, 65), (2, 801, 801), (2, 37, 200), (2, 129, 129),
+                                      (2, 801, 1), (1, 161, 70)])
+@pytest.mark.parametrize("odt", [BF16, F32])
+def test_attention_p_bf16(orc, dev, BH, nq, nk, odt):
+    say(f"attention P-bf16 BH={BH} nq={nq} nk={nk} out={odt}")
+    q = inp(orc, (BH, nq, 64), 0x4D425200B0, nq, BF16)
+    k = inp(orc, (BH, nk, 64), 0x4D425200B1, nk, BF16)
+    v = inp(orc, (BH, nk, 64), 0x4D425200B2, nk, BF16)
+    out = empty((BH, nq, 64), odt)
+    mbrt.attention(to_dev(q, BF16), to_dev(k, BF16), to_dev(v, BF16), out, 0.0, p_bf16=True)
+    torch.cuda.synchronize()
+    print("P-bf16 norm-wise", _assert_ref_p(orc, to_host(out, odt), q, k, v, odt, 0.0, "attention P-bf16"))
+
+
+def test_attention_p_bf16_known_answer(orc, dev):
+    """v = 1: out = sum bf16(p) / sum p per query, not 1 (the reference rounds P but not the
+    row sum); the oracle variant is pinned to that ratio on the CPU."""
+    say("attention P-bf16 with v = 1")
+    BH, nq, nk = 2, 40, 300
+    q = inp(orc, (BH, nq, 64), 0x4D425200B3, 0, BF16, std=2.0)
+    k = inp(orc, (BH, nk, 64), 0x4D425200B4, 0, BF16)
+    v = orc.from_f32(np.ones((BH, nk, 64), np.float32), BF16)
+    out = empty((BH, nq, 64), F32)
+    mbrt.attention(to_dev(q, BF16), to_dev(k, BF16), to_dev(v, BF16), out, 0.125, p_bf16=True)
+    torch.cuda.synchronize()
+    y = to_host(out, F32)
+    ref = orc.attention_ref_p(q, k, v, BF16, F32, 0.125)
+    assert np.abs(ref - 1).max() > 1e-5
+    assert np.abs(y - ref).max() <= 2.0 ** -7 / nk * 8 + 1e-6
+
+
+def test_attention_p_bf16_full_time_shape(orc, dev):
+    """The time attention [480, 801, 64] in the reference's arithmetic; every query of a
+    sample of heads against the oracle variant."""
+    say("attention P-bf16 full BH=480 N=801")
+    BH, N = 480, 801
+    g = torch.Generator(device="cuda").manual_seed(SEED[3] + 7)
+    q, k, v = (torch.randn((BH, N, 64), generator=g, device="cuda").to(torch.bfloat16) for _ in range(3))
+    out = torch.empty((BH, N, 64), dtype=torch.bfloat16, device="cuda")
+    mbrt.attention(q, k, v, out, 0.125, p_bf16=True)
+    torch.cuda.synchronize()
+    sel = torch.tensor(sorted(np.random.default_rng(6).choice(BH, 4, replace=False)), device="cuda")
+    qs, ks, vs = (to_host(t[sel], BF16) for t in (q, k, v))
+    _assert_ref_p(orc, to_host(out[sel], BF16), qs, ks, vs, BF16, 0.125, "attention P-bf16 full")
+
+
 @pytest.mark.parametrize("BH,N,scale", [(480, 801, 0.125), (6408, 60, 0.125)])
 def test_attention_full_shapes(orc, dev, BH, N, scale):
     """Time (480 heads x 801) and frequency (6408 x 60) attention at full chunk shape; the
@@ -733,6 +816,30 @@ def test_attention_bnhd_fusions(orc, dev, B, N, H, rot, gate, odt, tdt):
     if gate:
         gref = orc.gate_merge(to_host(att, odt), odt, g_h, BF16, odt, B, H, N, 64)
         assert_close(to_host(fused, odt), gref, odt, "attention_bnhd gate merge")
+
+
+def test_attention_bnhd_p_bf16_fusion(orc, dev):
+    """The reference's split-contig q-rotary time attention with the gate, in the
+    reference's P arithmetic: bit for bit rotary -> attention(P-bf16) -> gate merge."""
+    say("attention_bnhd P-bf16 rot+gate")
+    B, N, H = 2, 801, 8
+    qkv = to_dev(inp(orc, (B, N, 3 * H * 64), 0x4D425200B5, 0, BF16), BF16)
+    v5 = qkv.view(B, N, 3, H, 64)
+    q, k, v = v5[:, :, 0], v5[:, :, 1], v5[:, :, 2]
+    cos_h, sin_h = orc.rotary_tables(N, 64)
+    cos, sin = to_dev(cos_h, F32), to_dev(sin_h, F32)
+    g = to_dev(inp(orc, (B, N, H), 0x4D425200B6, 0, BF16, std=2.0), BF16)
+    fused = mbrt.attention_bnhd(q, k, v, cos=cos, sin=sin, gate=g, p_bf16=True)
+    qc, kc, vc = (t.permute(0, 2, 1, 3).contiguous().view(B * H, N, 64) for t in (q, k, v))
+    mbrt.rotary_(qc, None, cos, sin)
+    att = empty((B, H, N, 64), BF16)
+    mbrt.attention(qc, kc, vc, att.view(B * H, N, 64), 0.0, p_bf16=True)
+    sep = empty((B, N, H * 64), BF16)
+    mbrt.gate_merge(att, g, sep)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(fused, BF16), to_host(sep, BF16), "attention_bnhd P-bf16 = separate ops")
+    qh, kh, vh = (to_host(t[:2], BF16) for t in (qc, kc, vc))
+    _assert_ref_p(orc, to_host(att.view(B * H, N, 64)[:2], BF16), qh, kh, vh, BF16, 0.0, "bnhd P-bf16 attention")
 
 
 @pytest.mark.parametrize("gdt,logit,odt", [(F32, True, BF16), (F16, True, F32), (BF16, False, BF16),

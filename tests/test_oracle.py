@@ -468,6 +468,50 @@ def test_attention_matches_numpy_and_closed_forms(orc):
     assert np.allclose(orc.attention(q, orc.randn((1, 9, 64), seed=17), ones, F32, F32, 0.0), 3.0, atol=1e-6)
 
 
+def _bf16_round(x):
+    """float64 -> nearest bf16 (ties to even) by bit manipulation of the f32 value; the
+    inputs here are f32-exact products of exp, so one rounding of their f32 value is the
+    rounding of the value itself except at exact ties."""
+    f = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    f = (f + 0x7FFF + ((f >> 16) & 1)) >> 16 << 16
+    return f.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def test_attention_ref_p_pins(orc):
+    """The reference-P variant: (1) q = 0 makes every P exactly 1 (a bf16 value), so it
+    equals exact attention, the mean of v; (2) v = 1 gives sum bf16(p) / sum p per row,
+    rebuilt here from numpy scores with the same 64-key running max (0 if P or the row sum
+    were both rounded, or neither); (3) it stays within a bf16 rounding of every P of exact
+    attention, and is not equal to it."""
+    BH, nq, nk = 2, 9, 150
+    k = orc.randn((BH, nk, 64), seed=21)
+    v = orc.randn((BH, nk, 64), seed=22)
+    q0 = np.zeros((BH, nq, 64), np.float32)
+    assert_bitexact(orc.attention_ref_p(q0, k, v, F32, F32), orc.attention(q0, k, v, F32, F32), "q = 0")
+    q = orc.randn((BH, nq, 64), seed=23, std=2.0)
+    ones = np.ones((BH, nk, 64), np.float32)
+    got = orc.attention_ref_p(q, k, ones, F32, F32, 0.125)
+    s = np.einsum("bid,bjd->bij", q.astype(np.float64), k.astype(np.float64)) * 0.125
+    num = np.zeros((BH, nq))
+    den = np.zeros((BH, nq))
+    m = np.full((BH, nq), -np.inf)
+    for k0 in range(0, nk, 64):
+        st = s[..., k0:k0 + 64]
+        mn = np.maximum(m, st.max(-1))
+        a = np.exp(m - mn)
+        p = np.exp(st - mn[..., None])
+        num = num * a + _bf16_round(p).sum(-1)
+        den = den * a + p.sum(-1)
+        m = mn
+    ratio = num / den
+    assert np.abs(ratio - 1).max() > 1e-5  # the rounding is visible
+    assert np.allclose(got, np.broadcast_to(ratio[..., None], got.shape), rtol=0, atol=2e-7)
+    exact = orc.attention(q, k, v, F32, F32, 0.125)
+    refp = orc.attention_ref_p(q, k, v, F32, F32, 0.125)
+    rel = np.linalg.norm(refp - exact) / np.linalg.norm(exact)
+    assert 1e-5 < rel < 2.0 ** -8
+
+
 # ---- STFT / iSTFT --------------------------------------------------------------------------
 
 def _direct_stft(x, w, hop, center, norm):
