@@ -417,6 +417,21 @@ MBRT_API int mbrt_istft(const void* spec, int spec_dtype, const float* window, f
                         int64_t window_numel, int center, int normalized, int64_t length, void* workspace,
                         int64_t workspace_bytes, mbrt_stream_t stream);
 
+/* Bytes of device scratch the library holds on each GPU for mbrt_istft_noalloc. */
+#define MBRT_ISTFT_SCRATCH_BYTES (32 * 1024 * 1024)
+
+/* mbrt_istft with no workspace argument and no allocation of any kind: the block partials
+ * go to a scratch array the library holds on each GPU (MBRT_ISTFT_SCRATCH_BYTES, enough
+ * for mbrt_istft_workspace_bytes(batch, frames, hop) up to that size; larger calls fail
+ * with MBRT_E_SHAPE).  Every call on one GPU shares that array, so calls that overlap on
+ * one GPU (concurrent streams, threads) race.  Same results as mbrt_istft, bit for bit.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory,
+ * such as code under HIP graph capture and tight serving loops. */
+MBRT_API int mbrt_istft_noalloc(const void* spec, int spec_dtype, const float* window, float* out,
+                                int64_t batch, int64_t freq_bins, int64_t frames, int64_t n_fft, int64_t hop,
+                                int64_t win_length, int64_t window_numel, int center, int normalized,
+                                int64_t length, mbrt_stream_t stream);
+
 /* ---- chunk overlap-add --------------------------------------------------------- */
 
 /* dest[c, offset + i] += src[c, i] * window[i] for c < channels, i < chunk_len, and

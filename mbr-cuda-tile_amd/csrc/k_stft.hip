@@ -29,6 +29,8 @@
 //        zero fill are part of the same pass.  No atomics: the result is deterministic.
 #include "abi_common.hpp"
 
+#include <atomic>
+
 #include <cmath>
 
 namespace mbrt {
@@ -783,11 +785,45 @@ int64_t mbrt_istft_workspace_bytes(int64_t batch, int64_t frames, int64_t hop) {
     return batch * ceil_div(frames, kTF) * ((kTF - 1) * hop + kN) * (int64_t)sizeof(float);
 }
 
-int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out, int64_t batch,
+}  // extern "C"
+
+namespace {
+
+// Scratch of the allocation-free iSTFT (mbrt_istft_noalloc): the block partials of one
+// call.  A file-scope device array of MBRT_ISTFT_SCRATCH_BYTES, allocated on every GPU
+// that loads the library's code object and held until the process ends; all calls on one
+// GPU share it, so calls that overlap there race.  Nothing in it needs clearing: the block
+// pass writes every partial sample the final pass reads.  In host code `scratch` names a
+// host-side stand-in, not device memory: its device address on the current GPU is taken
+// once per device with hipGetSymbolAddress, and only that pointer reaches the kernels.
+__device__ __align__(256) float scratch[MBRT_ISTFT_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+
+int scratch_ptr(const char* op, void** ptr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    MBRT_REQUIRE(e == hipSuccess, MBRT_E_HIP, "%s: hipGetDevice: %s", op, hipGetErrorString(e));
+    MBRT_REQUIRE(dev >= 0 && dev < kMaxDevices, MBRT_E_HIP, "%s: device %d beyond %d", op, dev, kMaxDevices);
+    void* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        MBRT_REQUIRE(e == hipSuccess && p != nullptr, MBRT_E_HIP, "%s: hipGetSymbolAddress: %s", op,
+                     hipGetErrorString(e));
+        g_scratch[dev].store(p, std::memory_order_release);
+    }
+    *ptr = p;
+    return MBRT_OK;
+}
+
+// The two iSTFT passes over a workspace of block partials; `workspace` is NULL for the
+// allocation-free entry point, which then uses this GPU's scratch array.
+int istft_impl(const char* op, const void* spec, int spec_dtype, const float* window, float* out, int64_t batch,
                int64_t freq_bins, int64_t frames, int64_t n_fft, int64_t hop, int64_t win_length,
                int64_t window_numel, int center, int normalized, int64_t length, void* workspace,
                int64_t workspace_bytes, mbrt_stream_t stream) {
-    const char* op = "mbrt_istft";
+    const bool scratch = workspace == nullptr;
     int s = check_fixed_size(op, n_fft, win_length, window_numel);
     if (s != MBRT_OK) return s;
     MBRT_REQUIRE(freq_bins == kBins, MBRT_E_SHAPE, "%s: %lld frequency bins (expected 1025)", op,
@@ -799,8 +835,17 @@ int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out
                  (long long)hop);
     const int64_t out_len = mbrt_istft_output_length(frames, hop, center, length);
     if (batch == 0 || out_len == 0) return MBRT_OK;
-    MBRT_REQUIRE(spec && window && out && workspace, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
+    MBRT_REQUIRE(spec && window && out, MBRT_E_INVALID_ARG, "%s: NULL pointer", op);
     const int64_t need = mbrt_istft_workspace_bytes(batch, frames, hop);
+    if (scratch) {
+        MBRT_REQUIRE(need <= MBRT_ISTFT_SCRATCH_BYTES, MBRT_E_SHAPE,
+                     "%s: needs %lld bytes of scratch, more than the %lld the library holds per GPU (use mbrt_istft "
+                     "with a workspace)",
+                     op, (long long)need, (long long)MBRT_ISTFT_SCRATCH_BYTES);
+        s = scratch_ptr(op, &workspace);
+        if (s != MBRT_OK) return s;
+        workspace_bytes = MBRT_ISTFT_SCRATCH_BYTES;
+    }
     MBRT_REQUIRE(workspace_bytes >= need, MBRT_E_INVALID_ARG, "%s: workspace of %lld bytes, %lld needed", op,
                  (long long)workspace_bytes, (long long)need);
     MBRT_REQUIRE(aligned(workspace, 4) && aligned(spec, spec_dtype == F32 ? 8 : 4), MBRT_E_ALIGN,
@@ -843,6 +888,26 @@ int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out
     fa.offset = center ? kN / 2 : 0;
     hipLaunchKernelGGL(istft_final_kernel, dim3((unsigned)grid_for(out_len, 256)), dim3(256), 0, st, fa);
     return check_launch(op);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mbrt_istft(const void* spec, int spec_dtype, const float* window, float* out, int64_t batch,
+               int64_t freq_bins, int64_t frames, int64_t n_fft, int64_t hop, int64_t win_length,
+               int64_t window_numel, int center, int normalized, int64_t length, void* workspace,
+               int64_t workspace_bytes, mbrt_stream_t stream) {
+    if (workspace == nullptr) return set_error(MBRT_E_INVALID_ARG, "mbrt_istft: NULL workspace");
+    return istft_impl("mbrt_istft", spec, spec_dtype, window, out, batch, freq_bins, frames, n_fft, hop, win_length,
+                      window_numel, center, normalized, length, workspace, workspace_bytes, stream);
+}
+
+int mbrt_istft_noalloc(const void* spec, int spec_dtype, const float* window, float* out, int64_t batch,
+                       int64_t freq_bins, int64_t frames, int64_t n_fft, int64_t hop, int64_t win_length,
+                       int64_t window_numel, int center, int normalized, int64_t length, mbrt_stream_t stream) {
+    return istft_impl("mbrt_istft_noalloc", spec, spec_dtype, window, out, batch, freq_bins, frames, n_fft, hop,
+                      win_length, window_numel, center, normalized, length, nullptr, 0, stream);
 }
 
 }  // extern "C"

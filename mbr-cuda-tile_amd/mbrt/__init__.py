@@ -425,6 +425,21 @@ def istft(spec: torch.Tensor, window: torch.Tensor, hop: int, center: bool = Tru
     return out
 
 
+ISTFT_SCRATCH_BYTES = 32 * 1024 * 1024  # MBRT_ISTFT_SCRATCH_BYTES
+
+
+def istft_noalloc(spec: torch.Tensor, window: torch.Tensor, hop: int, out: torch.Tensor, center: bool = True,
+                  normalized: bool = False, length: int = -1, n_fft: int = N_FFT, win_length: int = N_FFT,
+                  stream=None) -> torch.Tensor:
+    """istft into a caller-provided `out` through mbrt_istft_noalloc: no workspace, no
+    allocation (the block partials use the library's scratch array on this GPU)."""
+    _contig(spec, window, out)
+    B, F, T, _ = spec.shape
+    _abi.call("mbrt_istft_noalloc", _p(spec), dtype_code(spec), _p(window), _p(out), B, F, T, n_fft, hop,
+              win_length, window.numel(), int(center), int(normalized), length, _s(stream))
+    return out
+
+
 def chunk_accumulate(dest: torch.Tensor, weight_sum: torch.Tensor, src: torch.Tensor, window: torch.Tensor,
                      offset: int, stream=None) -> torch.Tensor:
     """dest [.., L] += src [.., n] * window at `offset` (channels = src.numel() / n); weight_sum += window."""

@@ -104,6 +104,7 @@ SIGNATURES: dict[str, list] = {
     "mbrt_istft_output_length": [L, L, I, L],
     "mbrt_istft_workspace_bytes": [L, L, L],
     "mbrt_istft": [P, I, P, P, L, L, L, L, L, L, L, I, I, L, P, L, P],
+    "mbrt_istft_noalloc": [P, I, P, P, L, L, L, L, L, L, L, I, I, L, P],
     "mbrt_chunk_accumulate": [P, P, P, P, L, L, L, L, P],
     "mbrt_chunk_normalize": [P, P, L, L, P],
     "mbrt_chunk_fade_window": [P, L, L, I, I],
