@@ -75,10 +75,11 @@ __device__ __forceinline__ f32x2 load_complex(const void* p, int64_t i) {
     else return unpack_f16x2(w);
 }
 
-// Block (j-tile, t-tile, b).  Wave w reads tile rows jj = w, w+4, ..., w+60: the 64 frames
-// of stft row idx[j0+jj] (512 contiguous bytes).  The row index is loaded once per lane and
-// broadcast with readlane; indices are clamped into the tensors so the 16 loads of a lane
-// are unconditional and in flight together.
+// One tile per block (tensors whose element offsets exceed 32 bits).  Block (j-tile, t-tile,
+// b).  Wave w reads tile rows jj = w, w+4, ..., w+60: the 64 frames of stft row idx[j0+jj]
+// (512 contiguous bytes).  The row index is loaded once per lane and broadcast with
+// readlane; indices are clamped into the tensors so the 16 loads of a lane are
+// unconditional and in flight together.
 template <int ODT, bool I64>
 __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
     __shared__ f32x2 tile[kTJ][kTT + 1];
@@ -95,20 +96,13 @@ __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
     const f32x2* stft = reinterpret_cast<const f32x2*>(a.stft) + b * a.F * a.T + tq;
     constexpr int kR = kTJ / (kThreads / 64);  // 16 rows per wave
     f32x2 v[kR];
-    if constexpr (MBRT_BAND_SLOAD) {
-        // the row indices of a wave are uniform: scalar loads through the constant cache
-        int64_t f[kR];
+    // indices outside [0, F) read the nearest valid row
+    const int64_t fl = load_index(a.idx, I64, min(j0 + lane, a.J - 1));
+    const int f_lane = (int)min(max(fl, (int64_t)0), a.F - 1);
 #pragma unroll
-        for (int r = 0; r < kR; ++r) f[r] = ld_idx<I64>(a.idx, min(j0 + w + 4 * r, a.J - 1));
-#pragma unroll
-        for (int r = 0; r < kR; ++r) v[r] = gld<MBRT_NT_BAND>(stft + f[r] * a.T);
-    } else {
-        const int f_lane = ld_idx<I64>(a.idx, min(j0 + lane, a.J - 1));
-#pragma unroll
-        for (int r = 0; r < kR; ++r) {
-            const int64_t f = __builtin_amdgcn_readlane(f_lane, w + 4 * r);
-            v[r] = gld<MBRT_NT_BAND>(stft + f * a.T);
-        }
+    for (int r = 0; r < kR; ++r) {
+        const int64_t f = __builtin_amdgcn_readlane(f_lane, w + 4 * r);
+        v[r] = gld<MBRT_NT_BAND>(stft + f * a.T);
     }
 #pragma unroll
     for (int r = 0; r < kR; ++r) tile[w + 4 * r][lane] = v[r];
@@ -346,25 +340,12 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     const int t = t0 + lane;
     const int tq = min(t, a.T - 1);
 
-    // CSR offsets of the tile's freqs: uniform scalar loads, or lane l holds off[f0 + l]
-    int off_s[kPer + 1];
-    int off_lane = 0;
-    int e_begin, e_end;
-    if constexpr (MBRT_BAND_SLOAD) {
-        e_begin = ld_idx<I64>(a.off, f0);
-        e_end = ld_idx<I64>(a.off, f0 + nf);
-    } else {
-        off_lane = ld_idx<I64>(a.off, f0 + min(lane, nf));
-        e_begin = __builtin_amdgcn_readlane(off_lane, 0);
-        e_end = __builtin_amdgcn_readlane(off_lane, nf);
-    }
+    // CSR offsets of the tile's freqs: lane l holds off[f0 + l] (l <= nf), broadcast by readlane
+    const int off_lane = ld_idx<I64>(a.off, f0 + min(lane, nf));
+    const int e_begin = __builtin_amdgcn_readlane(off_lane, 0);
+    const int e_end = __builtin_amdgcn_readlane(off_lane, nf);
     float c = load1(a.cnt, a.cdt, f0 + min(lane, nf - 1));
     const float inv_lane = 1.0f / (c > 1.0e-8f ? c : 1.0e-8f);
-    if constexpr (MBRT_BAND_SLOAD) {
-#pragma unroll
-        for (int r = 0; r < kPer; ++r) off_s[r] = ld_idx<I64>(a.off, f0 + min(w + 4 * r, nf));
-        off_s[kPer] = 0;
-    }
 
     const f32x2* srow = reinterpret_cast<const f32x2*>(a.stft) + ((int64_t)b * a.F + f0) * a.T + tq;
     f32x2 sv[kPer], acc[kPer];
@@ -387,14 +368,8 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
             const int fl = w + 4 * r;  // local freq (wave-uniform); entries [off[f], off[f+1])
-            int lo, hi;
-            if constexpr (MBRT_BAND_SLOAD) {
-                lo = max(off_s[r], c0);
-                hi = fl < nf ? min(ld_idx<I64>(a.off, f0 + fl + 1), c1) : lo;
-            } else {
-                lo = max(__builtin_amdgcn_readlane(off_lane, fl), c0);
-                hi = fl < nf ? min(__builtin_amdgcn_readlane(off_lane, fl + 1), c1) : lo;
-            }
+            const int lo = max(__builtin_amdgcn_readlane(off_lane, fl), c0);
+            const int hi = fl < nf ? min(__builtin_amdgcn_readlane(off_lane, fl + 1), c1) : lo;
             for (int e = lo; e < hi; ++e) {
                 const f32x2 m = ms[e - c0][lane];
                 acc[r].x += sv[r].x * m.x - sv[r].y * m.y;

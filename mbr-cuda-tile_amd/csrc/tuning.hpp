@@ -61,9 +61,6 @@
 #ifndef MBRT_BAND_MERGE_TFAST
 #define MBRT_BAND_MERGE_TFAST 0  // band merge tile order: frame tiles fastest (1) or freq tiles fastest (0)
 #endif
-#ifndef MBRT_BAND_SLOAD
-#define MBRT_BAND_SLOAD 0  // band gather: row indices by scalar loads (1) or lane load + readlane (0)
-#endif
 #ifndef MBRT_SM_STAGE_LONG
 #define MBRT_SM_STAGE_LONG 1  // softmax rows of 129..1024 elements through LDS when spans align
 #endif

@@ -14,6 +14,14 @@ HipContext& HipContext::instance() {
 
 void HipContext::synchronize() const { HIP_CHECK(hipStreamSynchronize(stream_)); }
 
+void HipContext::set_stream(hipStream_t s) {
+    if (s == stream_) return;
+    // blocks freed while work on the old stream was pending may be handed out at once:
+    // that work must be done before anything runs on the new stream
+    HIP_CHECK(hipStreamSynchronize(stream_));
+    stream_ = s;
+}
+
 bool env_flag_enabled(const char* name) {
     const char* raw = std::getenv(name);
     if (raw == nullptr) return false;

@@ -29,12 +29,15 @@ extern bool g_quantize_bf16;
 // default stream with synchronous copies; here every op is enqueued on stream(), which
 // defaults to the null stream of the current device, and host<->device copies wait for it,
 // so the program order of Tensor calls is the execution order.  set_stream() moves all
-// later work to another stream; the caching allocator reuses blocks in that stream's order.
+// later work to another stream.  The caching allocator hands a freed block out again at
+// once, which is safe while all work runs on one stream (its order is the program order);
+// so set_stream() first waits for the work queued on the previous stream, after which no
+// block freed while that work was pending can be reused under it.
 class HipContext {
 public:
     static HipContext& instance();
     hipStream_t stream() const { return stream_; }
-    void set_stream(hipStream_t s) { stream_ = s; }
+    void set_stream(hipStream_t s);
     void synchronize() const;
 
 private:

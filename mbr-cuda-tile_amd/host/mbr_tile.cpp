@@ -4,6 +4,8 @@
 #include "mbr_tile.h"
 
 #include <algorithm>
+#include <atomic>
+#include <cstdio>
 #include <limits>
 #include <stdexcept>
 #include <string>
@@ -22,7 +24,9 @@ bool all_bf16_experiments() {
 bool remaining_bf16_experiments() {
     return g_quantize_bf16 && (custom_bf16_path() || env_flag_enabled("CUDASEP_REMAINING_BF16_EXPERIMENTS"));
 }
+void warn_full_bf16_arith();
 bool bf16_experiment(const char* name) {
+    warn_full_bf16_arith();
     return g_quantize_bf16 && (all_bf16_experiments() || env_flag_enabled(name));
 }
 bool remaining_bf16_experiment(const char* name) {
@@ -38,6 +42,16 @@ bool glu_bf16_input() { return remaining_bf16_experiment("CUDASEP_GLU_BF16_INPUT
 bool tanh_bf16_input() { return remaining_bf16_experiment("CUDASEP_TANH_BF16_INPUT"); }
 bool freq_attention60_padded() {
     return g_quantize_bf16 && !env_flag_enabled("CUDASEP_DISABLE_FREQ_ATTENTION60_CUTILE_PADDED");
+}
+// CUDASEP_FULL_BF16_ARITH_EXPERIMENTS (src/mbr_cuda_tile.cu:190-192) rounds intermediate
+// values (sums of squares, row maxima, exponentials, ...) to bf16 inside the reference's
+// kernels.  This library does not build that experiment: the switch is not honoured, and
+// the first policy query under bf16 says so once on stderr instead of ignoring it silently.
+void warn_full_bf16_arith() {
+    static std::atomic<bool> warned{false};
+    if (!warned.load(std::memory_order_relaxed) && g_quantize_bf16 &&
+        env_flag_enabled("CUDASEP_FULL_BF16_ARITH_EXPERIMENTS") && !warned.exchange(true))
+        std::fprintf(stderr, "[mbr_tile] CUDASEP_FULL_BF16_ARITH_EXPERIMENTS is not supported; ignored\n");
 }
 
 constexpr int kFreqAttnN = 60;
@@ -70,7 +84,12 @@ bool bands_per_freq_bf16_enabled() {
     return g_quantize_bf16 && !env_flag_enabled("CUDASEP_DISABLE_BANDS_PER_FREQ_BF16");
 }
 bool rotary_freqs_bf16_enabled() { return g_quantize_bf16 && !env_flag_enabled("CUDASEP_DISABLE_ROTARY_FREQS_BF16"); }
-bool residual_rms_norm_fused_path_enabled() { return !env_flag_enabled("CUDASEP_DISABLE_RESIDUAL_RMS_NORM_FUSED"); }
+// The reference's predicate (src/mbr_cuda_tile.cu:166-169, 6000-6002): the model takes its
+// fused feed-forward branch (src/model_mel_band_roformer.cu:490) only under bf16.  The
+// fused op itself, try_residual_add_rms_norm, serves every dtype unless disabled.
+bool residual_rms_norm_fused_path_enabled() {
+    return g_quantize_bf16 && !env_flag_enabled("CUDASEP_DISABLE_RESIDUAL_RMS_NORM_FUSED");
+}
 
 // ---- normalisation ----------------------------------------------------------------------
 
@@ -90,7 +109,7 @@ Tensor rms_norm(const Tensor& x, const Tensor& gamma, float scale) {
 
 bool try_residual_add_rms_norm(const Tensor& residual, const Tensor& update, const Tensor& gamma, float scale,
                                Tensor& residual_out, Tensor& normed) {
-    if (!residual_rms_norm_fused_path_enabled()) return false;
+    if (env_flag_enabled("CUDASEP_DISABLE_RESIDUAL_RMS_NORM_FUSED")) return false;
     if (residual.dtype() != update.dtype() || !is_float(residual.dtype())) return false;
     if (residual.shape() != update.shape() || residual.ndim() == 0 || residual.numel() == 0) return false;
     if (!residual.is_contiguous() || !update.is_contiguous()) return false;

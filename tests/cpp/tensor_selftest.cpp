@@ -228,6 +228,26 @@ void unit() {
     check(after.cache_hits >= before.cache_hits + 1, "freed block is reused");
     pool.trim_cached_memory();
     check(pool.get_stats().cached_bytes == 0, "trim releases the cache");
+
+    // set_stream: the work queued on the old stream is done before any work on the new
+    // one, so a block freed under pending work cannot be reused while that work runs
+    {
+        auto& ctx = cudasep::HipContext::instance();
+        hipStream_t s1 = nullptr, s2 = nullptr;
+        HIP_CHECK(hipStreamCreate(&s1));
+        HIP_CHECK(hipStreamCreate(&s2));
+        ctx.set_stream(s1);
+        Tensor big = Tensor::empty({1 << 26});
+        big.fill_(1.0f);
+        for (int i = 0; i < 8; ++i) big.add_(big);  // queued work on s1
+        { Tensor freed = big + big; }  // its block goes back to the cache with work pending on s1
+        ctx.set_stream(s2);
+        check(hipStreamQuery(s1) == hipSuccess, "set_stream waits for the previous stream");
+        check(same(big.slice(0, 0, 4).to_cpu_f32(), std::vector<float>(4, 256.0f)), "work of the old stream kept");
+        ctx.set_stream(nullptr);
+        HIP_CHECK(hipStreamDestroy(s1));
+        HIP_CHECK(hipStreamDestroy(s2));
+    }
 }
 
 // ---- ops mode: raw little-endian inputs/outputs named in <dir>/manifest.txt -------------
@@ -470,7 +490,7 @@ void csm(const std::string& path) {
     }
     // malformed files: each load must throw; the message is recorded
     std::ofstream errs(path + "/errors.txt");
-    for (const char* bad : {"bad_magic", "bad_version", "truncated", "bad_dtype", "missing"}) {
+    for (const char* bad : {"bad_magic", "bad_version", "truncated", "bad_dtype", "missing", "huge_bytes", "huge_numel"}) {
         try {
             (void)ModelWeights::load(path + "/" + bad + ".csm");
             errs << bad << " LOADED\n";

@@ -282,6 +282,16 @@ def test_csm_loader_json_and_band_tables(orc, dev, tmp_path):
     bd = bytearray((tmp_path / "bad_dtype.csm").read_bytes())
     struct.pack_into("<I", bd, len(bd) - 8 - 4, 9)  # dtype field of the only tensor
     (tmp_path / "bad_dtype.csm").write_bytes(bytes(bd))
+    # shapes whose element count (huge_numel) or byte count (huge_bytes) overflows int64:
+    # the header alone says so, before any allocation or read
+    csm.write_csm(tmp_path / "huge_bytes.csm", {}, [("w", np.ones(2, np.float32))])
+    hb = bytearray((tmp_path / "huge_bytes.csm").read_bytes())
+    struct.pack_into("<q", hb, len(hb) - 8 - 4 - 8, 2**62)  # the only dim: 2^62 f32 = 2^64 bytes
+    (tmp_path / "huge_bytes.csm").write_bytes(bytes(hb))
+    csm.write_csm(tmp_path / "huge_numel.csm", {}, [("w", np.ones((1, 2), np.float32))])
+    hn = bytearray((tmp_path / "huge_numel.csm").read_bytes())
+    struct.pack_into("<qq", hn, len(hn) - 8 - 4 - 16, 2**33, 2**33)  # 2^66 elements
+    (tmp_path / "huge_numel.csm").write_bytes(bytes(hn))
     (tmp_path / "json_cases.txt").write_text("\n".join(JSON_CASES) + "\n", encoding="utf-8")
 
     r = _selftest("csm", str(tmp_path))
@@ -318,6 +328,8 @@ def test_csm_loader_json_and_band_tables(orc, dev, tmp_path):
     assert errs["bad_magic"] == "ModelWeights: invalid magic (expected CSM\\0)"
     assert errs["bad_version"] == "ModelWeights: unsupported version 3"
     assert errs["truncated"].startswith("ModelWeights: unexpected EOF")
+    assert errs["huge_bytes"] == "ModelWeights: tensor too large: w"
+    assert errs["huge_numel"] == "ModelWeights: tensor too large: w"
     assert errs["bad_dtype"] == "ModelWeights: unknown dtype 9 for tensor w"
     assert errs["missing"].startswith("ModelWeights: cannot open file: ")
     outs = (tmp_path / "json_out.txt").read_text(encoding="utf-8").splitlines()
