@@ -41,7 +41,7 @@ METRIC = "achieved HBM GB/s (% of MI355X peak) per op; ms of tensor ops per chun
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
 MALL_DEFEAT_BYTES = 1.1e9
-TRAFFIC_SUMMARY = REPO / "profiles" / "traffic_softmax_time_f32.md"
+TRAFFIC_SUMMARY = REPO / "profiles" / "traffic_all_ops.md"
 
 
 def parse_args():
@@ -332,13 +332,13 @@ def band_tables(torch, mbrt):
     return t(fi), t(off), t(ind), t(cnt)
 
 
-def read_traffic():
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), if present."""
+def read_traffic() -> dict:
+    """HBM bytes per launch of every op, from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated with a copy of known size); {} if absent."""
     if not TRAFFIC_SUMMARY.exists():
-        return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_SUMMARY.read_text(), flags=re.M)
-    return float(m.group(1)) if m else None
+        return {}
+    return {m.group(1): float(m.group(2)) for m in
+            re.finditer(r"^traffic_bytes_per_launch\[(\w+)\]:\s*([0-9.eE+]+)", TRAFFIC_SUMMARY.read_text(), flags=re.M)}
 
 
 def cpu_model() -> str:
@@ -506,6 +506,14 @@ def main():
     next_ops = {}
     tot_bytes = 0
     tot_ms = 0.0
+    traffic = read_traffic()
+
+    def with_traffic(entry, op):
+        if op.name in traffic:
+            entry["traffic"] = traffic[op.name]
+            entry["traffic_over_algorithmic"] = round(traffic[op.name] / op.bytes, 4)
+        return entry
+
     for op in [o for o in ops if o.next]:
         ms = op.ms
         gbs = op.bytes / (ms * 1e-3) / 1e9
@@ -521,6 +529,7 @@ def main():
         else:
             next_ops[op.name] = {"bytes": op.bytes, "ms": round(ms, 5), "gbs": round(gbs, 1),
                                  "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "kernel": op.kernel}
+        with_traffic(next_ops[op.name], op)
     ops = [o for o in ops if not o.next]
     for op in ops:
         ms = op.ms
@@ -532,6 +541,7 @@ def main():
         if op.copy_ms:
             per_op[op.name]["copy_same_bytes_gbs"] = round(op.bytes / (op.copy_ms * 1e-3) / 1e9, 1)
             per_op[op.name]["frac_of_same_size_copy"] = round(op.copy_ms / ms, 4)
+        with_traffic(per_op[op.name], op)
         if op.retimed:
             per_op[op.name]["retimed"] = op.retimed
         if gbs > HBM_PEAK_GBS:  # inputs are cycled past the MALL: this can only be a measurement error
@@ -590,7 +600,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": read_traffic() if dom.name == "bl3_softmax_time_f32" else None,
+            "traffic": traffic.get(dom.name),
             "algorithmic_bytes": dom.bytes,
             "avg_ms": round(dom_ms, 5),
         },

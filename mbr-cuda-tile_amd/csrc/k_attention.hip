@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
                     for (int i = 0; i < 4; ++i)
                         if (kt + 16 * kb + 4 * g + i >= a.nk) st[x][kb][i] = -INFINITY;
         }
-        if constexpr (PM == MBRT_ATTN_P_BF16 && !MBRT_ATTN_PBF16_LAZY) {
+        if constexpr (PM == MBRT_ATTN_P_BF16) {
             // the reference's running max: m[x] = max(m[x], max of the tile's scaled scores)
             // every tile, the accumulator and row sum rescaled by exp2(m_old - m_new)
 #pragma unroll

@@ -73,9 +73,6 @@
 #ifndef MBRT_SM_SHORT_RPG
 #define MBRT_SM_SHORT_RPG 2  // rows per lane group in those blocks
 #endif
-#ifndef MBRT_ATTN_PBF16_LAZY
-#define MBRT_ATTN_PBF16_LAZY 0  // P-bf16 attention: the lazy running max of the pair mode (1) instead of the reference's per-tile max (0)
-#endif
 #ifndef MBRT_ACT_U
 #define MBRT_ACT_U 2     // 16-byte groups per thread: bias + activation (GELU)
 #endif
