@@ -16,6 +16,8 @@
 // Rows longer than 64 x 32 elements use a three-pass loop kernel.
 #include "abi_common.hpp"
 
+#include <type_traits>
+
 #include <algorithm>
 #include <cfloat>
 
@@ -86,10 +88,18 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
 template <int IDT, int ODT, int G, int NM, int RPG>
 __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
     constexpr int RB = RPG * kThreads / G;
+    // rows of more than 128 elements (groups of 32 or 64 lanes) have their own cache policy
+    constexpr int NT = G >= 32 ? MBRT_NT_SML : MBRT_NT_SMS;
     constexpr int VI = 16 / DtSize<IDT>::value, VO = 16 / DtSize<ODT>::value;
-    constexpr int CAP = RB * G * NM;  // floats of LDS (RB rows of at most G*NM elements)
+    constexpr int CAP = RB * G * NM;  // elements of LDS (RB rows of at most G*NM elements)
     constexpr int KI = (CAP / VI + kThreads - 1) / kThreads, KO = (CAP / VO + kThreads - 1) / kThreads;
-    __shared__ float buf[CAP];
+    // bf16 -> bf16 and f16 -> f16 spans stay in their 2-byte format in LDS: 16-byte vectors
+    // move in and out unchanged (no 32-byte-per-lane f32 staging, which conflicts on the
+    // LDS banks), and the probabilities are rounded where they are written back, exactly
+    // where the f32 staging would round them on the way out
+    constexpr bool K16 = IDT == ODT && IDT != F32 && MBRT_SM_STAGE16;
+    using Elem = typename std::conditional<K16, uint16_t, float>::type;
+    __shared__ __attribute__((aligned(16))) Elem buf[CAP];
     const int tid = threadIdx.x;
     const int64_t row0 = (int64_t)blockIdx.x * RB;
     const int nrows = (int)min((int64_t)RB, a.rows - row0);
@@ -98,18 +108,32 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
     const int nvi = nel / VI;
     Vec<IDT, VI> iv[KI];
 #pragma unroll
-    for (int k = 0; k < KI; ++k) iv[k].template load<MBRT_NT_SMS>(a.in, ebase + (int64_t)min(tid + kThreads * k, nvi - 1) * VI);
+    for (int k = 0; k < KI; ++k) iv[k].template load<NT>(a.in, ebase + (int64_t)min(tid + kThreads * k, nvi - 1) * VI);
 #pragma unroll
     for (int k = 0; k < KI; ++k) {
         const int v = tid + kThreads * k;
         if (v < nvi) {
-            float f[VI];
-            iv[k].to_f32(f);
+            if constexpr (K16) {
+                *reinterpret_cast<u32x4*>(&buf[v * VI]) = u32x4{iv[k].w[0], iv[k].w[1], iv[k].w[2], iv[k].w[3]};
+            } else {
+                float f[VI];
+                iv[k].to_f32(f);
 #pragma unroll
-            for (int i = 0; i < VI; ++i) buf[v * VI + i] = f[i];
+                for (int i = 0; i < VI; ++i) buf[v * VI + i] = f[i];
+            }
         }
     }
     __syncthreads();
+    auto get = [&](int e) -> float {
+        if constexpr (!K16) return buf[e];
+        else if constexpr (IDT == BF16) return __uint_as_float((uint32_t)buf[e] << 16);
+        else return (float)__builtin_bit_cast(_Float16, buf[e]);
+    };
+    auto put = [&](int e, float v) {
+        if constexpr (!K16) buf[e] = v;
+        else if constexpr (IDT == BF16) buf[e] = f32_to_bf16_bits(v);
+        else buf[e] = f32_to_f16_bits(v);
+    };
     const int lane = tid % G;
     const int last = a.cols - 1;
 #pragma unroll
@@ -120,7 +144,7 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
         float m = -INFINITY;
 #pragma unroll
         for (int k = 0; k < NM; ++k) {
-            const float x = buf[rbase + min(lane + G * k, last)];
+            const float x = get(rbase + min(lane + G * k, last));
             z[k] = lane + G * k <= last ? x * a.scale_log2e : -INFINITY;
             m = fmaxf(m, z[k]);
         }
@@ -136,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
         if (r < nrows) {
 #pragma unroll
             for (int k = 0; k < NM; ++k)
-                if (lane + G * k <= last) buf[rbase + lane + G * k] = z[k] * inv;
+                if (lane + G * k <= last) put(rbase + lane + G * k, z[k] * inv);
         }
     }
     __syncthreads();
@@ -145,12 +169,17 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
     for (int k = 0; k < KO; ++k) {
         const int v = tid + kThreads * k;
         if (v < nvo) {
-            float f[VO];
-#pragma unroll
-            for (int i = 0; i < VO; ++i) f[i] = buf[v * VO + i];
             Vec<ODT, VO> o;
-            o.from_f32(f);
-            o.template store<MBRT_NT_SMS>(a.out, ebase + (int64_t)v * VO);
+            if constexpr (K16) {
+                const u32x4 t = *reinterpret_cast<const u32x4*>(&buf[v * VO]);
+                o.w[0] = t.x; o.w[1] = t.y; o.w[2] = t.z; o.w[3] = t.w;
+            } else {
+                float f[VO];
+#pragma unroll
+                for (int i = 0; i < VO; ++i) f[i] = buf[v * VO + i];
+                o.from_f32(f);
+            }
+            o.template store<NT>(a.out, ebase + (int64_t)v * VO);
         }
     }
 }
@@ -205,16 +234,18 @@ bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) 
     else if (c <= 64 && fits(32)) launch_staged<IDT, 8, 8>(a, st);
     else if (c <= 128 && fits(16)) launch_staged<IDT, 16, 8>(a, st);
     else if (c <= 128 || !MBRT_SM_STAGE_LONG) return false;
-    else if (MBRT_SM_LONG_G == 64 && fits(4)) {
-        if (c <= 256) launch_staged<IDT, 64, 4>(a, st);
-        else if (c <= 512) launch_staged<IDT, 64, 8>(a, st);
-        else if (c <= 832) launch_staged<IDT, 64, 13>(a, st);
-        else launch_staged<IDT, 64, 16>(a, st);
-    } else if (fits(8)) {
-        if (c <= 256) launch_staged<IDT, 32, 8>(a, st);
-        else if (c <= 512) launch_staged<IDT, 32, 16>(a, st);
-        else if (c <= 832) launch_staged<IDT, 32, 26>(a, st);
-        else launch_staged<IDT, 32, 32>(a, st);
+    else if (MBRT_SM_LONG_G == 64 && fits(4 * MBRT_SM_LONG_RPG)) {
+        constexpr int R = MBRT_SM_LONG_RPG;
+        if (c <= 256) launch_staged<IDT, 64, 4, R>(a, st);
+        else if (c <= 512) launch_staged<IDT, 64, 8, R>(a, st);
+        else if (c <= 832) launch_staged<IDT, 64, 13, R>(a, st);
+        else launch_staged<IDT, 64, 16, R>(a, st);
+    } else if (fits(8 * MBRT_SM_LONG_RPG)) {
+        constexpr int R = MBRT_SM_LONG_RPG;
+        if (c <= 256) launch_staged<IDT, 32, 8, R>(a, st);
+        else if (c <= 512) launch_staged<IDT, 32, 16, R>(a, st);
+        else if (c <= 832) launch_staged<IDT, 32, 26, R>(a, st);
+        else launch_staged<IDT, 32, 32, R>(a, st);
     } else {
         return false;
     }

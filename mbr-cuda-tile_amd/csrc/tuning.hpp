@@ -27,6 +27,9 @@
 #ifndef MBRT_NT_SMS
 #define MBRT_NT_SMS 3    // LDS-staged short softmax rows (freq attention, 60 columns)
 #endif
+#ifndef MBRT_NT_SML
+#define MBRT_NT_SML 3    // LDS-staged long softmax rows (time attention, 801 columns)
+#endif
 #ifndef MBRT_NT_ROT
 #define MBRT_NT_ROT 3    // rotary q/k
 #endif
@@ -66,6 +69,12 @@
 #endif
 #ifndef MBRT_SM_LONG_G
 #define MBRT_SM_LONG_G 64  // lanes per staged row of 129..1024 elements when 4-row spans align (64 or 32)
+#endif
+#ifndef MBRT_SM_STAGE16
+#define MBRT_SM_STAGE16 1  // staged softmax: bf16->bf16 / f16->f16 spans kept 2-byte in LDS (1) or as f32 (0)
+#endif
+#ifndef MBRT_SM_LONG_RPG
+#define MBRT_SM_LONG_RPG 1  // staged softmax rows of 129..1024 elements: rows per lane group (block of 4 or 8 rows x this)
 #endif
 #ifndef MBRT_SM_SHORT_BYTES
 #define MBRT_SM_SHORT_BYTES 6144  // staged softmax rows of 33..64: below this many input bytes per 32 rows, 64-row blocks
