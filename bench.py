@@ -74,6 +74,8 @@ class Op:
         self.ms = 0.0            # mean GPU time per call over the timed calls
         self.retimed = 0         # timings redone because the host enqueue outlasted the hold
         self.copy_ms = 0.0       # a plain copy of the same bytes, timed the same way
+        self.mix = None          # "r1w2": also compared with a contiguous kernel of the same read/write mix
+        self.mix_ms = 0.0
 
 
 def build_ops(torch, mbrt, bands):
@@ -155,8 +157,9 @@ def build_ops(torch, mbrt, bands):
     Bb, F, T = 4, 2050, 801
     J = fi.numel()
     op = Op("bl5a_band_gather_f32", Bb * F * T * 2 * 4 + Bb * T * J * 2 * 4 + J * 4,
-            lambda: dict(s=randn((Bb, F, T, 2)), y=torch.empty((Bb, T, J * 2), device=dev)), "band_gather_kernel")
+            lambda: dict(s=randn((Bb, F, T, 2)), y=torch.empty((Bb, T, J * 2), device=dev)), "band_gather_pipe_kernel")
     op.run = lambda b: mbrt.band_gather(b["s"], fi, b["y"])
+    op.mix = "r1w2"  # reads the stft once (52.5 MB), writes twice as much (101.4 MB)
     ops.append(op)
     op = Op("bl5b_band_mask_merge_f32",
             Bb * T * J * 2 * 4 + Bb * F * T * 2 * 4 + Bb * 2 * (F // 2) * T * 2 * 4 + (off.numel() + J) * 4 + F * 4,
@@ -167,16 +170,18 @@ def build_ops(torch, mbrt, bands):
     # Fused attention (MFMA), the first widening beyond the tensor-op path: q, k, v bf16
     # [BH, N, 64] for the time (480 x 801) and frequency (6408 x 60) attention.  Reported in
     # config.next_ops with TFLOP/s (4 BH N^2 64 flop); not part of `value`.
-    for atag, abh, an, pb in (("time", 480, 801, False), ("freq", 6408, 60, False), ("time", 480, 801, True),
-                              ("freq", 6408, 60, True)):
-        op = Op(f"attention_{atag}_bf16" + ("_p_bf16" if pb else ""), 4 * abh * an * 64 * 2,
+    P_SUFFIX = {mbrt.ATTN_P_PAIR: "", mbrt.ATTN_P_BF16: "_p_bf16", mbrt.ATTN_P_BF16_FAST: "_p_bf16_fast"}
+    for atag, abh, an, pb in (("time", 480, 801, mbrt.ATTN_P_PAIR), ("freq", 6408, 60, mbrt.ATTN_P_PAIR),
+                              ("time", 480, 801, mbrt.ATTN_P_BF16), ("freq", 6408, 60, mbrt.ATTN_P_BF16),
+                              ("time", 480, 801, mbrt.ATTN_P_BF16_FAST), ("freq", 6408, 60, mbrt.ATTN_P_BF16_FAST)):
+        op = Op(f"attention_{atag}_bf16" + P_SUFFIX[pb], 4 * abh * an * 64 * 2,
                 (lambda abh=abh, an=an: dict(q=randn((abh, an, 64), bf16), k=randn((abh, an, 64), bf16),
                                              v=randn((abh, an, 64), bf16),
                                              y=torch.empty((abh, an, 64), dtype=bf16, device=dev))),
                 "attention_kernel")
         op.flops = 4.0 * abh * an * an * 64
         op.next = True
-        op.run = lambda b, pb=pb: mbrt.attention(b["q"], b["k"], b["v"], b["y"], 0.125, p_bf16=pb)
+        op.run = lambda b, pb=pb: mbrt.attention(b["q"], b["k"], b["v"], b["y"], 0.125, p_precision=pb)
         ops.append(op)
     # The time attention as the reference's split-contig q-rotary form plus the gate: q, k, v
     # read in place from the fused qkv projection [60, 801, 3*8*64], q rotated in the kernel,
@@ -298,6 +303,17 @@ def copy_op(torch, mbrt, nbytes):
     return op
 
 
+def mix_op(torch, mbrt, nbytes):
+    """A contiguous kernel that reads one third and writes two thirds of `nbytes`: the
+    library's bf16 -> f32 conversion.  The ceiling for ops with that read/write mix."""
+    n = max(8, int(nbytes) // 6 // 8 * 8)
+    op = Op(f"mix_r1w2_{nbytes}", n * 6,
+            lambda: dict(x=torch.empty(n, dtype=torch.bfloat16, device="cuda"), y=torch.empty(n, device="cuda")),
+            "convert_vec_kernel")
+    op.run = lambda b: mbrt.convert(b["x"], b["y"])
+    return op
+
+
 def copy_ceiling(torch, mbrt, args):
     """--copy-ceiling: copy rate by size, and the time of a one-element launch (the fixed
     cost every kernel pays between back-to-back calls on one stream)."""
@@ -318,7 +334,20 @@ def copy_ceiling(torch, mbrt, args):
               file=sys.stderr, flush=True)
         op.sets = []
         torch.cuda.empty_cache()
-    print(json.dumps({"copy_ceiling": rows, "launch_1_element_us": round(tiny.ms * 1e3, 3),
+    mix_rows = []
+    for mb in (50, 100, 150, 200, 400):
+        op = mix_op(torch, mbrt, int(mb * 1e6))
+        make_sets(op)
+        time_op(op)
+        mix_rows.append({"bytes_moved": op.bytes, "us": round(op.ms * 1e3, 2),
+                         "gbs": round(op.bytes / (op.ms * 1e-3) / 1e9, 1)})
+        print(f"read 1 : write 2 {op.bytes / 1e6:8.1f} MB moved: {op.ms * 1e3:8.2f} us  {mix_rows[-1]['gbs']:7.1f} GB/s",
+              file=sys.stderr, flush=True)
+        op.sets = []
+        torch.cuda.empty_cache()
+    print(json.dumps({"copy_ceiling": rows, "read1_write2_ceiling": mix_rows,
+                      "read1_write2_kernel": "bf16 -> f32 convert_kernel",
+                      "launch_1_element_us": round(tiny.ms * 1e3, 3),
                       "kernel": "row_copy_kernel<16, 2>", "steps": args.steps,
                       "mall_defeat": f"buffer sets cycled past {MALL_DEFEAT_BYTES / 1e9:.1f} GB"}), flush=True)
 
@@ -500,6 +529,12 @@ def main():
             time_op(c)
             op.copy_ms = c.ms
             c.sets = []
+            if op.mix == "r1w2":
+                c = mix_op(torch, mbrt, op.bytes)
+                make_sets(c)
+                time_op(c)
+                op.mix_ms = c.ms
+                c.sets = []
         torch.cuda.empty_cache()
 
     per_op = {}
@@ -541,6 +576,9 @@ def main():
         if op.copy_ms:
             per_op[op.name]["copy_same_bytes_gbs"] = round(op.bytes / (op.copy_ms * 1e-3) / 1e9, 1)
             per_op[op.name]["frac_of_same_size_copy"] = round(op.copy_ms / ms, 4)
+        if op.mix_ms:
+            per_op[op.name]["read1_write2_same_bytes_gbs"] = round(op.bytes / (op.mix_ms * 1e-3) / 1e9, 1)
+            per_op[op.name]["frac_of_same_mix_kernel"] = round(op.mix_ms / ms, 4)
         with_traffic(per_op[op.name], op)
         if op.retimed:
             per_op[op.name]["retimed"] = op.retimed

@@ -354,16 +354,20 @@ MBRT_API int mbrt_attention_strided(const void* q, const void* k, const void* v,
 /* Precision of the probabilities P in the attention's second product (O = P V). */
 enum mbrt_attn_precision {
     MBRT_ATTN_P_PAIR = 0, /* P as a bf16 hi + lo pair: f32 accuracy (mbrt_attention's default) */
-    MBRT_ATTN_P_BF16 = 1  /* the reference's arithmetic: running max per 64-key tile, P
+    MBRT_ATTN_P_BF16 = 1, /* the reference's arithmetic: running max per 64-key tile, P
                              rounded once to bf16 for one P V product, the row sum over
                              the unrounded P (src/mbr_time_attention_cutile.cu:160-180) */
+    MBRT_ATTN_P_BF16_FAST = 2 /* P rounded once to bf16 as in MBRT_ATTN_P_BF16, but the
+                                 running max moves only when a 64-key tile's max exceeds it
+                                 by 8 (log2 units), and the row sum adds the rounded P (an
+                                 MFMA against ones): the fastest mode, same error size */
 };
 
 /* mbrt_attention_strided with the P precision chosen (enum mbrt_attn_precision).
  * MBRT_ATTN_P_BF16 runs one MFMA per key tile instead of two and matches the
  * reference's rounding of P; its output differs from exact attention by ~1e-3 of the
- * output's RMS (one bf16 rounding of every P).  Replaces the same reference functions
- * as mbrt_attention_strided. */
+ * output's RMS (one bf16 rounding of every P); MBRT_ATTN_P_BF16_FAST likewise.
+ * Replaces the same reference functions as mbrt_attention_strided. */
 MBRT_API int mbrt_attention_ex(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
                                int64_t n_q, int64_t n_k, int64_t head_dim, int64_t q_batch_stride,
                                int64_t q_head_stride, int64_t q_row_stride, int64_t kv_batch_stride,

@@ -41,6 +41,9 @@ constexpr int kQWave = 16;     // queries per wave
 constexpr int kWaves = 4;
 constexpr int kQBlock = kQWave * kWaves;
 constexpr float kLazy = 8.0f;  // log2 units the running max may outgrow the exponent reference
+#ifndef MBRT_ATTN_WPE
+#define MBRT_ATTN_WPE 4  // waves per SIMD the register budget is sized for (4: at most 128 VGPRs)
+#endif
 #ifndef MBRT_ATTN_QS2_MIN
 #define MBRT_ATTN_QS2_MIN 1  // 32 queries per wave when n_q exceeds this many 64-query blocks
 #endif
@@ -78,10 +81,55 @@ struct AttnArgs {
     int glogit;         // the gate holds logits: sigmoid(gate) multiplies
 };
 
-__device__ __forceinline__ float xor_max(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16));
-    return fmaxf(x, __shfl_xor(x, 32));
+// Maxima of finite-or-infinite scores with the raw v_max instructions: fmaxf makes the
+// compiler quiet possible signalling NaNs first (one v_max x, x per operand), which the
+// scores of an MFMA never are.
+__device__ __forceinline__ float vmax(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+// max of the 16 scores a lane holds for one 16-query sub-block
+__device__ __forceinline__ float max16(const f32x4 (&s)[4]) {
+    const float a = vmax3(s[0][0], s[0][1], s[0][2]), b = vmax3(s[0][3], s[1][0], s[1][1]);
+    const float c = vmax3(s[1][2], s[1][3], s[2][0]), d = vmax3(s[2][1], s[2][2], s[2][3]);
+    const float e = vmax3(s[3][0], s[3][1], s[3][2]);
+    return vmax(vmax3(a, b, c), vmax3(d, e, s[3][3]));
+}
+__device__ __forceinline__ float xor_max(float x) {
+    x = vmax(x, __shfl_xor(x, 16));
+    return vmax(x, __shfl_xor(x, 32));
+}
+// The eight V^T transpose reads of one 32-key chunk (four 16-column blocks db, rows r and
+// r + 16 each) at LDS byte addresses ad[db] + OFF and ad[db] + OFF + 2048, issued together
+// and completed before the statement ends: the compiler, short of registers, would
+// otherwise interleave them with the MFMAs and wait for each pair on its own.
+template <int OFF>
+__device__ __forceinline__ void lds_read_vt(const uint32_t (&ad)[4], bf16x8 (&va)[4]) {
+    u32x2 r[8];
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %8 offset:%[lo]\n\t"
+        "ds_read_b64_tr_b16 %1, %8 offset:%[hi]\n\t"
+        "ds_read_b64_tr_b16 %2, %9 offset:%[lo]\n\t"
+        "ds_read_b64_tr_b16 %3, %9 offset:%[hi]\n\t"
+        "ds_read_b64_tr_b16 %4, %10 offset:%[lo]\n\t"
+        "ds_read_b64_tr_b16 %5, %10 offset:%[hi]\n\t"
+        "ds_read_b64_tr_b16 %6, %11 offset:%[lo]\n\t"
+        "ds_read_b64_tr_b16 %7, %11 offset:%[hi]\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+        : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), [lo] "n"(OFF), [hi] "n"(OFF + 2048)
+        : "memory");
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+        va[db] = __builtin_bit_cast(bf16x8, u32x4{r[2 * db].x, r[2 * db].y, r[2 * db + 1].x, r[2 * db + 1].y});
+}
+
 __device__ __forceinline__ float xor_sum(float x) {
     x += __shfl_xor(x, 16);
     return x + __shfl_xor(x, 32);
@@ -90,11 +138,14 @@ __device__ __forceinline__ float xor_sum(float x) {
 // QS = 16-query sub-blocks per wave (1 or 2): every K and V^T fragment read from LDS
 // feeds QS MFMAs, so longer sequences use QS = 2 (128 queries per workgroup).
 // PM = precision of P in the second product: MBRT_ATTN_P_PAIR (P as a bf16 hi + lo pair,
-// f32 accuracy, lazy max) or MBRT_ATTN_P_BF16 (the reference's arithmetic,
+// f32 accuracy, lazy max), MBRT_ATTN_P_BF16 (the reference's arithmetic,
 // src/mbr_time_attention_cutile.cu:160-180: the running max moves every 64-key tile, P is
-// rounded once to bf16 for one P V product, and the row sum adds the unrounded P).
+// rounded once to bf16 for one P V product, and the row sum adds the unrounded P) or
+// MBRT_ATTN_P_BF16_FAST (P rounded once to bf16 under the lazy max, and the row sum formed
+// by the MFMA from the same rounded P, as a 17th block of V columns that are all 1: no
+// rescale on most tiles and no VALU row sum).
 template <int ODT, int QS, int PM>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBRT_ATTN_WPE))) void attention_kernel(AttnArgs a) {
     // two K and two V tiles: the next pair is loaded (straight into LDS) while the current
     // one is read
     __shared__ __attribute__((aligned(16))) __bf16 k0[kKeys * kHeadDim];
@@ -159,15 +210,21 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
         }
     }
 
+    constexpr bool kLazyMax = PM != MBRT_ATTN_P_BF16;
+    constexpr bool kSumMfma = PM == MBRT_ATTN_P_BF16_FAST;
     f32x4 o[QS][4];
+    f32x4 osum[QS];  // kSumMfma: lane (g, c) holds the row sum of query c, four times
     float m[QS], l[QS];
 #pragma unroll
     for (int x = 0; x < QS; ++x) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[x][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        osum[x] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         m[x] = -INFINITY;
         l[x] = 0.0f;
     }
+    // A operand of the row-sum MFMA: a 16 x 32 block of bf16 ones
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
     // Tile loads go from HBM straight into LDS (global_load_lds_dwordx4: lane i of a wave
     // instruction writes the 16 bytes at base + 16 i).  Wave w loads keys 16w .. 16w + 15 of
@@ -225,16 +282,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
                     for (int i = 0; i < 4; ++i)
                         if (kt + 16 * kb + 4 * g + i >= a.nk) st[x][kb][i] = -INFINITY;
         }
-        if constexpr (PM == MBRT_ATTN_P_BF16) {
+        if constexpr (!kLazyMax) {
             // the reference's running max: m[x] = max(m[x], max of the tile's scaled scores)
             // every tile, the accumulator and row sum rescaled by exp2(m_old - m_new)
 #pragma unroll
             for (int x = 0; x < QS; ++x) {
-                float mx = -INFINITY;
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-                    mx = fmaxf(mx, fmaxf(fmaxf(st[x][kb][0], st[x][kb][1]), fmaxf(st[x][kb][2], st[x][kb][3])));
-                const float mn = fmaxf(m[x], xor_max(mx) * a.scale_log2e);
+                const float mx = max16(st[x]);
+                const float mn = vmax(m[x], xor_max(mx) * a.scale_log2e);
                 const float alpha = __builtin_amdgcn_exp2f(m[x] - mn);
                 l[x] *= alpha;
 #pragma unroll
@@ -258,10 +312,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
             // P <= 2^kLazy otherwise, harmless in f32 and in the bf16 pair, and the
             // accumulator is rescaled about once per query.  The lane's own 16 scores decide
             // whether to look; the max over the query's four lanes is formed only then.
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-                mx = fmaxf(mx, fmaxf(fmaxf(st[x][kb][0], st[x][kb][1]), fmaxf(st[x][kb][2], st[x][kb][3])));
+            float mx = max16(st[x]);
             // wave-uniform branch, taken on the (rare) tiles where some score of the wave
             // outgrows its reference; queries that do not grow keep alpha = 1
             if (__builtin_amdgcn_ballot_w64(mx * a.scale_log2e > m[x] + kLazy) != 0) {
@@ -269,19 +320,20 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
                 const float mn = mx > m[x] + kLazy ? mx : m[x];
                 const float alpha = __builtin_amdgcn_exp2f(m[x] - mn);
                 l[x] *= alpha;
+                osum[x] *= alpha;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) o[x][db] *= alpha;
                 m[x] = mn;
             }
             // l[x] is the lane's partial row sum over its own keys; the four lanes of a
-            // query are added once, after the last tile
+            // query are added once, after the last tile (the MFMA forms it when kSumMfma)
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float p = __builtin_amdgcn_exp2f(fmaf(st[x][kb][i], a.scale_log2e, -m[x]));
                     st[x][kb][i] = p;
-                    l[x] += p;
+                    if constexpr (!kSumMfma) l[x] += p;
                 }
             }
         }
@@ -301,7 +353,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
                     for (int i = 0; i < 4; i += 2) {
                         const float p0 = st[x][2 * cc + h][i], p1 = st[x][2 * cc + h][i + 1];
-                        if constexpr (PM == MBRT_ATTN_P_BF16) {
+                        if constexpr (PM != MBRT_ATTN_P_PAIR) {
                             hw[2 * h + i / 2] = pack_bf16x2(p0, p1);  // one RNE rounding
                         } else {
                             const uint32_t b0 = __float_as_uint(p0) & 0xffff0000u;
@@ -312,22 +364,30 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
                     }
                 }
                 ph[x] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
-                if constexpr (PM != MBRT_ATTN_P_BF16) pl[x] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+                if constexpr (PM == MBRT_ATTN_P_PAIR) pl[x] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+                if constexpr (kSumMfma) osum[x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, ph[x], osum[x], 0, 0, 0);
             }
+            // V^T operand by LDS transpose reads: in each 16-lane group, lane i receives
+            // element i%4 of the 8-byte chunks of lanes 4r + i/4 (r = 0..3), so lane
+            // (g, c) supplies V[32cc + 4g + c/4 (+16)][16db + 4(c%4) ..] and receives
+            // V[32cc + 4g + r (+16)][16db + c] for r = 0..3: slots j and 4 + j.  The
+            // eight reads of a chunk are issued together, ahead of its MFMAs (rows 32cc
+            // and 16 further are 4096 and 2048 bytes on; the chunk swizzle depends on
+            // the row mod 8 only).
+            uint32_t vad[4];
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                vad[db] = lds_addr(vs) + 2 * (uint32_t)tile_at(4 * g + (c >> 2), 2 * db + ((c & 3) >> 1), 4 * (c & 1));
+            bf16x8 vat[4];
+            if (cc == 0) lds_read_vt<0>(vad, vat);
+            else lds_read_vt<4096>(vad, vat);
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                // V^T operand by LDS transpose reads: in each 16-lane group, lane i receives
-                // element i%4 of the 8-byte chunks of lanes 4r + i/4 (r = 0..3), so lane
-                // (g, c) supplies V[32cc + 4g + c/4 (+16)][16db + 4(c%4) ..] and receives
-                // V[32cc + 4g + r (+16)][16db + c] for r = 0..3: slots j and 4 + j.
-                const int vrow = 32 * cc + 4 * g + (c >> 2), vch = 2 * db + ((c & 3) >> 1), vin = 4 * (c & 1);
-                const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(&vs[tile_at(vrow, vch, vin)]));
-                const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(&vs[tile_at(vrow + 16, vch, vin)]));
-                const bf16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                const bf16x8 va = vat[db];
 #pragma unroll
                 for (int x = 0; x < QS; ++x) {
                     o[x][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[x], o[x][db], 0, 0, 0);
-                    if constexpr (PM != MBRT_ATTN_P_BF16)
+                    if constexpr (PM == MBRT_ATTN_P_PAIR)
                         o[x][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[x], o[x][db], 0, 0, 0);
                 }
             }
@@ -340,7 +400,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
 
 #pragma unroll
     for (int x = 0; x < QS; ++x) {
-        const float lsum = xor_sum(l[x]);
+        const float lsum = kSumMfma ? osum[x][0] : xor_sum(l[x]);
         const int q = q0 + 16 * x + c;
         if (q >= a.nq) continue;
         const float inv = 1.0f / lsum;
@@ -397,8 +457,9 @@ int mbrt_attention_ex(const void* q, const void* k, const void* v, int dtype, in
                       int gate_is_logit, void* out, int out_dtype, float scale, int p_precision,
                       mbrt_stream_t stream) {
     const char* op = "mbrt_attention";
-    MBRT_REQUIRE(p_precision == MBRT_ATTN_P_PAIR || p_precision == MBRT_ATTN_P_BF16, MBRT_E_INVALID_ARG,
-                 "%s: unknown P precision %d", op, p_precision);
+    MBRT_REQUIRE(p_precision == MBRT_ATTN_P_PAIR || p_precision == MBRT_ATTN_P_BF16 ||
+                     p_precision == MBRT_ATTN_P_BF16_FAST,
+                 MBRT_E_INVALID_ARG, "%s: unknown P precision %d", op, p_precision);
     MBRT_REQUIRE(dtype == BF16, MBRT_E_UNSUPPORTED_DTYPE, "%s: q/k/v must be BF16", op);
     MBRT_REQUIRE(out_dtype == BF16 || out_dtype == F32, MBRT_E_UNSUPPORTED_DTYPE, "%s: out must be BF16/F32", op);
     MBRT_REQUIRE(head_dim == kHeadDim, MBRT_E_SHAPE, "%s: head_dim %lld (only 64 is built)", op, (long long)head_dim);
@@ -471,6 +532,7 @@ int mbrt_attention_ex(const void* q, const void* k, const void* v, int dtype, in
         }
     };
     if (p_precision == MBRT_ATTN_P_BF16) launch(std::integral_constant<int, MBRT_ATTN_P_BF16>{});
+    else if (p_precision == MBRT_ATTN_P_BF16_FAST) launch(std::integral_constant<int, MBRT_ATTN_P_BF16_FAST>{});
     else launch(std::integral_constant<int, MBRT_ATTN_P_PAIR>{});
     return check_launch(op);
 }

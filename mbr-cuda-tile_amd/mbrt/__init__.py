@@ -314,31 +314,41 @@ def zero_dc(spec: torch.Tensor, stream=None) -> torch.Tensor:
     return spec
 
 
-ATTN_P_PAIR, ATTN_P_BF16 = 0, 1  # enum mbrt_attn_precision
+ATTN_P_PAIR, ATTN_P_BF16, ATTN_P_BF16_FAST = 0, 1, 2  # enum mbrt_attn_precision
+
+
+def _p_precision(p_bf16: bool, p_precision: int | None) -> int:
+    if p_precision is None:
+        return ATTN_P_BF16 if p_bf16 else ATTN_P_PAIR
+    if p_bf16 and p_precision != ATTN_P_BF16:
+        raise ValueError("attention: p_bf16 and p_precision disagree")
+    return int(p_precision)
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor, scale: float = 0.0,
-              p_bf16: bool = False, stream=None) -> torch.Tensor:
+              p_bf16: bool = False, stream=None, p_precision: int | None = None) -> torch.Tensor:
     """Fused attention: q [BH, nq, 64], k, v [BH, nk, 64] bf16 -> out [BH, nq, 64] (bf16/f32).
-    p_bf16 selects the reference's arithmetic (P rounded once to bf16 for P V)."""
+    p_bf16 selects the reference's arithmetic (P rounded once to bf16 for P V);
+    p_precision one of ATTN_P_PAIR / ATTN_P_BF16 / ATTN_P_BF16_FAST."""
     for t in (q, k, v, out):
         _contig(t)
     BH, nq, D = q.shape
     nk = k.shape[1]
-    if not p_bf16:
+    pm = _p_precision(p_bf16, p_precision)
+    if pm == ATTN_P_PAIR:
         _abi.call("mbrt_attention", _p(q), _p(k), _p(v), dtype_code(q), _p(out), dtype_code(out), BH, nq, nk, D,
                   float(scale), _s(stream))
     else:
         _abi.call("mbrt_attention_ex", _p(q), _p(k), _p(v), dtype_code(q), BH, 1, nq, nk, D, nq * D, 0, D,
                   nk * D, 0, D, None, None, F32, None, F32, 0, _p(out), dtype_code(out), float(scale),
-                  ATTN_P_BF16, _s(stream))
+                  pm, _s(stream))
     return out
 
 
 def attention_bnhd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor | None = None,
                    scale: float = 0.0, cos: torch.Tensor | None = None, sin: torch.Tensor | None = None,
                    gate: torch.Tensor | None = None, gate_is_logit: bool = True, out_dtype=None,
-                   p_bf16: bool = False, stream=None) -> torch.Tensor:
+                   p_bf16: bool = False, stream=None, p_precision: int | None = None) -> torch.Tensor:
     """Fused attention over [B, N, H, 64] bf16 views (any strides with a unit last dim, e.g.
     slices of a fused qkv projection).  cos, sin [n_q, 32] rotate q in-kernel.  Without a
     gate the result is [B, H, n_q, 64]; with gate [B, n_q, H] it is the gated head merge
@@ -362,7 +372,7 @@ def attention_bnhd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch
               _p(cos) if cos is not None else None, _p(sin) if sin is not None else None,
               dtype_code(cos) if cos is not None else F32,
               _p(gate) if gate is not None else None, dtype_code(gate) if gate is not None else F32,
-              int(gate_is_logit), _p(out), dtype_code(out), float(scale), ATTN_P_BF16 if p_bf16 else ATTN_P_PAIR,
+              int(gate_is_logit), _p(out), dtype_code(out), float(scale), _p_precision(p_bf16, p_precision),
               _s(stream))
     return out
 

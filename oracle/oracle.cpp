@@ -745,8 +745,8 @@ void orc_attention(const void* q, const void* k, const void* v, int dt, void* ou
 // m moves to the max of each tile's scaled scores; P = exp(s - m) is rounded once to bf16
 // for the P V sum while the row sum l adds the unrounded P; both are rescaled by
 // exp(m_old - m_new); out = O / l rounded once to odt.
-void orc_attention_ref_p(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
-                         int64_t nq, int64_t nk, int64_t D, float scale) {
+void orc_attention_ref_p_ex(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
+                            int64_t nq, int64_t nk, int64_t D, float scale, double lazy, int sum_rounded) {
     const double sc = scale == 0.0f ? 1.0 / std::sqrt((double)D) : (double)scale;
     const int64_t kTile = 64;
 #pragma omp parallel for schedule(static) num_threads(g_threads)
@@ -765,20 +765,27 @@ void orc_attention_ref_p(const void* q, const void* k, const void* v, int dt, vo
                 s[j] = acc * sc;
                 tm = std::max(tm, s[j]);
             }
-            const double mn = std::max(m, tm);
+            // the running max moves to the tile's max when that exceeds it by more than
+            // `lazy` (0: every tile, the exact running max)
+            const double mn = tm > m + lazy ? tm : m;
             const double alpha = std::exp(m - mn);
             l *= alpha;
             for (int64_t d = 0; d < D; ++d) o[d] *= alpha;
             m = mn;
             for (int64_t j = 0; j < n; ++j) {
                 const double p = std::exp(s[j] - m);
-                l += p;
                 const double pb = (double)bf16_to_f32(f64_to_bf16(p));
+                l += sum_rounded ? pb : p;
                 for (int64_t d = 0; d < D; ++d) o[d] += pb * (double)ld(v, dt, kb0 + (k0 + j) * D + d);
             }
         }
         for (int64_t d = 0; d < D; ++d) st(out, odt, r * D + d, o[d] / l);
     }
+}
+
+void orc_attention_ref_p(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
+                         int64_t nq, int64_t nk, int64_t D, float scale) {
+    orc_attention_ref_p_ex(q, k, v, dt, out, odt, BH, nq, nk, D, scale, 0.0, 0);
 }
 
 }  // extern "C"

@@ -91,6 +91,11 @@ void orc_attention(const void* q, const void* k, const void* v, int dt, void* ou
 /* the time attention with the reference's rounding of P (src/mbr_time_attention_cutile.cu:160-180) */
 void orc_attention_ref_p(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
                          int64_t nq, int64_t nk, int64_t D, float scale);
+/* the same with the running max moved only when a 64-key tile's max exceeds it by more
+ * than `lazy` (natural-log units; 0 = every tile), and the row sum over the rounded P when
+ * sum_rounded (the library's MBRT_ATTN_P_BF16_FAST: lazy = 8 ln 2, sum_rounded = 1) */
+void orc_attention_ref_p_ex(const void* q, const void* k, const void* v, int dt, void* out, int odt, int64_t BH,
+                            int64_t nq, int64_t nk, int64_t D, float scale, double lazy, int sum_rounded);
 
 #ifdef __cplusplus
 }

@@ -9,6 +9,7 @@ BF16=3, I32=4).
 from __future__ import annotations
 
 import ctypes as C
+import math
 import subprocess
 from pathlib import Path
 
@@ -308,14 +309,24 @@ def attention(q, k, v, dt, odt, scale=0.0, mode=EXACT):
     return out
 
 
-def attention_ref_p(q, k, v, dt, odt, scale=0.0):
+def attention_ref_p(q, k, v, dt, odt, scale=0.0, lazy=0.0, sum_rounded=False):
     """The attention with the reference's P arithmetic: running max per 64-key tile, P
-    rounded once to bf16 for P V, row sum over the unrounded P (double elsewhere)."""
+    rounded once to bf16 for P V, row sum over the unrounded P (double elsewhere).  With
+    lazy > 0 the running max moves only when a tile's max exceeds it by more than `lazy`
+    (natural-log units); sum_rounded adds the rounded P to the row sum."""
     BH, nq, D = q.shape
     nk = k.shape[1]
     out = empty((BH, nq, D), odt)
-    lib().orc_attention_ref_p(_p(q), _p(k), _p(v), dt, _p(out), odt, L(BH), L(nq), L(nk), L(D), C.c_float(scale))
+    if lazy == 0.0 and not sum_rounded:
+        lib().orc_attention_ref_p(_p(q), _p(k), _p(v), dt, _p(out), odt, L(BH), L(nq), L(nk), L(D), C.c_float(scale))
+    else:
+        lib().orc_attention_ref_p_ex(_p(q), _p(k), _p(v), dt, _p(out), odt, L(BH), L(nq), L(nk), L(D),
+                                     C.c_float(scale), C.c_double(lazy), int(sum_rounded))
     return out
+
+
+# the library's fast bf16-P mode: the running max moves by more than 8 in log2 units
+ATTN_FAST_LAZY = 8.0 * math.log(2.0)
 
 
 # ---- STFT / iSTFT, n_fft = win_length = 2048 (src/stft_cuda_tile.cu) ----------------------

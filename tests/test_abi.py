@@ -111,7 +111,7 @@ def test_widened_entry_points_reject_bad_arguments_without_gpu(lib):
     assert strided(cos=p) == 1 and "cos and sin" in _err(lib)
     assert lib.mbrt_attention(p, p, p, bf16, p, f32, 4, 8, 8, 32, 0.0, None) == 3
     assert lib.mbrt_attention_ex(p, p, p, bf16, 1, 2, 8, 8, 64, 8 * 192, 64, 192, 8 * 192, 64, 192, None, None, f32,
-                                 None, bf16, 1, p, f32, 0.0, 2, None) == 1 and "precision" in _err(lib)
+                                 None, bf16, 1, p, f32, 0.0, 3, None) == 1 and "precision" in _err(lib)
 
     def stft(batch=1, length=4096, n_fft=2048, hop=441, win=2048, numel=2048, center=1, sig=p, out=p):
         return lib.mbrt_stft(sig, p, out, batch, length, n_fft, hop, win, numel, center, 0, None)

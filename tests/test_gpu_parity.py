@@ -527,7 +527,8 @@ def test_band_gather_bl5a_full(orc, dev, idt, odt):
 
 
 # Ragged shapes and every length of the gather's persistent tile walk (1, 2, 3 and more
-# tiles per block on a 256-CU device): random indices with repeats, every output dtype.
+# tiles per block on a 256-CU device): random indices with repeats, every output dtype,
+# two frames, and 16000 band-bins (250 band-bin tiles).
 @pytest.mark.parametrize("B,F,T,J,idt,odt,seed", [
     (1, 2050, 801, 3958, I32, F32, 1),
     (3, 70, 1, 5, I32, F32, 2),
@@ -537,7 +538,9 @@ def test_band_gather_bl5a_full(orc, dev, idt, odt):
     (2, 100, 64, 1, I32, F32, 6),
     (8, 2050, 64, 3958, I64, F32, 7),
     (12, 2050, 64, 3958, I32, F32, 8),
-    (1, 7, 200, 129, I32, F32, 9)])
+    (1, 7, 200, 129, I32, F32, 9),
+    (2, 300, 2, 100, I64, BF16, 10),
+    (1, 500, 45, 16000, I32, F32, 11)])
 def test_band_gather_shapes(orc, dev, B, F, T, J, idt, odt, seed):
     say(f"band gather B={B} F={F} T={T} J={J} idx={idt} out={odt}")
     rng = np.random.default_rng(seed)
@@ -679,7 +682,7 @@ def _pmax_v(q, k, v, scale):
     return np.max(p[..., :, None] * np.abs(vd)[:, None, :, :], axis=2)
 
 
-def _assert_ref_p(orc, y, q, k, v, odt, scale, what):
+def _assert_ref_p(orc, y, q, k, v, odt, scale, what, fast=False):
     """The reference-P attention against the oracle variant that restates its rounding.  The
     kernel's P (f32 exp2) and the oracle's (double exp) round to different bf16 neighbours
     only within a few f32 ulps of a rounding boundary; each such flip moves an output by at
@@ -688,7 +691,10 @@ def _assert_ref_p(orc, y, q, k, v, odt, scale, what):
     (2e-3 for bf16 outputs, the usual rule).  Against exact attention it is within one
     bf16 rounding of every P: norm-wise 2^-8."""
     qf, kf, vf = (orc.to_f32(t, BF16) for t in (q, k, v))
-    ref = orc.attention_ref_p(q, k, v, BF16, odt, scale)
+    if fast:  # the fast mode's rounding: lazy running max, row sum over the rounded P
+        ref = orc.attention_ref_p(q, k, v, BF16, odt, scale, lazy=orc.ATTN_FAST_LAZY, sum_rounded=True)
+    else:
+        ref = orc.attention_ref_p(q, k, v, BF16, odt, scale)
     den = orc.attention(qf, kf, np.abs(vf), F32, F32, scale).astype(np.float64)
     pm = _pmax_v(qf, kf, vf, scale)
     a, b = orc.to_f32(y, odt).astype(np.float64), orc.to_f32(ref, odt).astype(np.float64)
@@ -734,6 +740,55 @@ def test_attention_p_bf16_known_answer(orc, dev):
     ref = orc.attention_ref_p(q, k, v, BF16, F32, 0.125)
     assert np.abs(ref - 1).max() > 1e-5
     assert np.abs(y - ref).max() <= 2.0 ** -7 / nk * 8 + 1e-6
+
+
+@pytest.mark.parametrize("BH,nq,nk", [(3, 1, 1), (2, 65, 65), (2, 801, 801), (2, 37, 200), (2, 129, 129),
+                                      (2, 801, 1), (1, 161, 70), (2, 300, 700)])
+@pytest.mark.parametrize("odt", [BF16, F32])
+def test_attention_p_bf16_fast(orc, dev, BH, nq, nk, odt):
+    say(f"attention P-bf16 fast BH={BH} nq={nq} nk={nk} out={odt}")
+    q = inp(orc, (BH, nq, 64), 0x4D425200C0, nq, BF16, std=1.5)
+    k = inp(orc, (BH, nk, 64), 0x4D425200C1, nk, BF16)
+    v = inp(orc, (BH, nk, 64), 0x4D425200C2, nk, BF16)
+    if nk >= 700:
+        # keys aligned with the queries far down the sequence: the running max has to move
+        kq = orc.to_f32(k, BF16)
+        kq[:, nk - 100:nk - 100 + min(nq, 100)] = 0.6 * orc.to_f32(q, BF16)[:, :min(nq, 100)]
+        k = orc.from_f32(kq, BF16)
+    out = empty((BH, nq, 64), odt)
+    mbrt.attention(to_dev(q, BF16), to_dev(k, BF16), to_dev(v, BF16), out, 0.0, p_precision=mbrt.ATTN_P_BF16_FAST)
+    torch.cuda.synchronize()
+    print("P-bf16 fast norm-wise", _assert_ref_p(orc, to_host(out, odt), q, k, v, odt, 0.0, "attention P-bf16 fast",
+                                                 fast=True))
+
+
+def test_attention_p_bf16_fast_known_answer(orc, dev):
+    """v = 1: the output and the row sum add the same rounded P in the same order, so every
+    output is 1 up to the final division (one f32 rounding)."""
+    say("attention P-bf16 fast with v = 1")
+    BH, nq, nk = 2, 40, 300
+    q = inp(orc, (BH, nq, 64), 0x4D425200C3, 0, BF16, std=2.0)
+    k = inp(orc, (BH, nk, 64), 0x4D425200C4, 0, BF16)
+    v = orc.from_f32(np.ones((BH, nk, 64), np.float32), BF16)
+    out = empty((BH, nq, 64), F32)
+    mbrt.attention(to_dev(q, BF16), to_dev(k, BF16), to_dev(v, BF16), out, 0.125, p_precision=mbrt.ATTN_P_BF16_FAST)
+    torch.cuda.synchronize()
+    assert np.abs(to_host(out, F32) - 1.0).max() <= 2.0 ** -23
+
+
+def test_attention_p_bf16_fast_full_time_shape(orc, dev):
+    """The time attention [480, 801, 64] in the fast bf16-P mode; every query of a sample
+    of heads against the oracle variant."""
+    say("attention P-bf16 fast full BH=480 N=801")
+    BH, N = 480, 801
+    g = torch.Generator(device="cuda").manual_seed(SEED[3] + 9)
+    q, k, v = (torch.randn((BH, N, 64), generator=g, device="cuda").to(torch.bfloat16) for _ in range(3))
+    out = torch.empty((BH, N, 64), dtype=torch.bfloat16, device="cuda")
+    mbrt.attention(q, k, v, out, 0.125, p_precision=mbrt.ATTN_P_BF16_FAST)
+    torch.cuda.synchronize()
+    sel = torch.tensor(sorted(np.random.default_rng(7).choice(BH, 4, replace=False)), device="cuda")
+    qs, ks, vs = (to_host(t[sel], BF16) for t in (q, k, v))
+    _assert_ref_p(orc, to_host(out[sel], BF16), qs, ks, vs, BF16, 0.125, "attention P-bf16 fast full", fast=True)
 
 
 def test_attention_p_bf16_full_time_shape(orc, dev):

@@ -512,6 +512,39 @@ def test_attention_ref_p_pins(orc):
     assert 1e-5 < rel < 2.0 ** -8
 
 
+def test_attention_ref_p_fast_pins(orc):
+    """The fast bf16-P variant (running max moved only past 8 log2 units, row sum over the
+    rounded P): (1) v = 1 gives exactly 1, the row sum and the output adding the same
+    rounded values; (2) when every query's largest score lies in the first 64-key tile the
+    running max never moves in either rule, so it equals the every-tile rule with the
+    rounded row sum bit for bit; (3) with later tiles that outgrow the first by more than
+    8 log2 units (the max must move), it stays within a bf16 rounding of every P of exact
+    attention, and differs from the every-tile rule."""
+    lazy = orc.ATTN_FAST_LAZY
+    assert abs(lazy - 8 * np.log(2)) < 1e-15
+    BH, nq, nk = 2, 9, 200
+    k = orc.randn((BH, nk, 64), seed=31)
+    v = orc.randn((BH, nk, 64), seed=32)
+    q = orc.randn((BH, nq, 64), seed=33, std=2.0)
+    ones = np.ones((BH, nk, 64), np.float32)
+    got = orc.attention_ref_p(q, k, ones, F32, F32, 0.125, lazy=lazy, sum_rounded=True)
+    assert_bitexact(got, np.ones_like(got), "v = 1")
+    k1 = k.copy()
+    k1[:, :nq] = 3.0 * q  # each query's largest score is its own key, in the first tile
+    a = orc.attention_ref_p(q, k1, v, F32, F32, 0.125, lazy=lazy, sum_rounded=True)
+    b = orc.attention_ref_p(q, k1, v, F32, F32, 0.125, lazy=0.0, sum_rounded=True)
+    assert_bitexact(a, b, "max in the first tile")
+    k2 = k.copy()
+    k2[:, 130:130 + nq] = 0.5 * q  # the largest scores in the third tile, 7 to 16 above the first
+    s = np.einsum("bid,bjd->bij", q.astype(np.float64), k2.astype(np.float64)) * 0.125
+    assert (s[..., 128:].max(-1) - s[..., :64].max(-1)).min() > lazy  # every row's max moves
+    a = orc.attention_ref_p(q, k2, v, F32, F32, 0.125, lazy=lazy, sum_rounded=True)
+    b = orc.attention_ref_p(q, k2, v, F32, F32, 0.125, lazy=0.0, sum_rounded=True)
+    exact = orc.attention(q, k2, v, F32, F32, 0.125)
+    assert np.linalg.norm(a - exact) / np.linalg.norm(exact) < 2.0 ** -8
+    assert np.abs(a - b).max() > 0
+
+
 # ---- STFT / iSTFT --------------------------------------------------------------------------
 
 def _direct_stft(x, w, hop, center, norm):
