@@ -346,9 +346,9 @@ def copy_ceiling(torch, mbrt, args):
         op.sets = []
         torch.cuda.empty_cache()
     print(json.dumps({"copy_ceiling": rows, "read1_write2_ceiling": mix_rows,
-                      "read1_write2_kernel": "bf16 -> f32 convert_kernel",
+                      "read1_write2_kernel": "bf16 -> f32 convert_vec_kernel",
                       "launch_1_element_us": round(tiny.ms * 1e3, 3),
-                      "kernel": "row_copy_kernel<16, 2>", "steps": args.steps,
+                      "kernel": "row_copy_kernel<16, 1>", "steps": args.steps,
                       "mall_defeat": f"buffer sets cycled past {MALL_DEFEAT_BYTES / 1e9:.1f} GB"}), flush=True)
 
 

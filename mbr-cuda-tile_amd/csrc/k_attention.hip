@@ -81,29 +81,19 @@ struct AttnArgs {
     int glogit;         // the gate holds logits: sigmoid(gate) multiplies
 };
 
-// Maxima of finite-or-infinite scores with the raw v_max instructions: fmaxf makes the
-// compiler quiet possible signalling NaNs first (one v_max x, x per operand), which the
-// scores of an MFMA never are.
-__device__ __forceinline__ float vmax(float a, float b) {
-    float r;
-    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-// max of the 16 scores a lane holds for one 16-query sub-block
+// max of the 16 scores a lane holds for one 16-query sub-block (the file is built without
+// NaN semantics, so the maxima need no quieting and fold into v_max3)
 __device__ __forceinline__ float max16(const f32x4 (&s)[4]) {
-    const float a = vmax3(s[0][0], s[0][1], s[0][2]), b = vmax3(s[0][3], s[1][0], s[1][1]);
-    const float c = vmax3(s[1][2], s[1][3], s[2][0]), d = vmax3(s[2][1], s[2][2], s[2][3]);
-    const float e = vmax3(s[3][0], s[3][1], s[3][2]);
-    return vmax(vmax3(a, b, c), vmax3(d, e, s[3][3]));
+    float m = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, s[kb][i]);
+    return m;
 }
 __device__ __forceinline__ float xor_max(float x) {
-    x = vmax(x, __shfl_xor(x, 16));
-    return vmax(x, __shfl_xor(x, 32));
+    x = fmaxf(x, __shfl_xor(x, 16));
+    return fmaxf(x, __shfl_xor(x, 32));
 }
 // The eight V^T transpose reads of one 32-key chunk (four 16-column blocks db, rows r and
 // r + 16 each) at LDS byte addresses ad[db] + OFF and ad[db] + OFF + 2048, issued together
@@ -288,7 +278,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBR
 #pragma unroll
             for (int x = 0; x < QS; ++x) {
                 const float mx = max16(st[x]);
-                const float mn = vmax(m[x], xor_max(mx) * a.scale_log2e);
+                const float mn = fmaxf(m[x], xor_max(mx) * a.scale_log2e);
                 const float alpha = __builtin_amdgcn_exp2f(m[x] - mn);
                 l[x] *= alpha;
 #pragma unroll

@@ -95,7 +95,7 @@
 #define MBRT_EW_U 4      // 16-byte groups per thread in the elementwise kernels
 #endif
 #ifndef MBRT_ROW_U
-#define MBRT_ROW_U 2     // row-copy vectors per thread
+#define MBRT_ROW_U 1     // row-copy vectors per thread
 #endif
 #ifndef MBRT_RMS_G
 #define MBRT_RMS_G 16    // lanes per row for rows of at most 128 16-byte chunks (16 or 32)

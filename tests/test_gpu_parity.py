@@ -437,11 +437,12 @@ def test_softmax_shapes(orc, dev, cols, idt, odt):
 
 @pytest.mark.parametrize("rows,cols", [(1000, 16), (1000, 17), (1000, 32), (1000, 60), (1000, 100), (1000, 128),
                                        (2008, 60), (8, 60), (1000, 200), (96, 513), (1000, 801), (24, 801),
-                                       (1000, 1024)])
+                                       (1000, 1024), (1001, 516), (7000, 516), (13001, 520)])
 @pytest.mark.parametrize("idt,odt", [(F32, F32), (BF16, BF16), (F32, BF16), (BF16, F32), (F16, F16)])
 def test_softmax_short_rows(orc, dev, rows, cols, idt, odt):
     """Row counts whose spans are whole 16-byte vectors (the LDS-staged path, up to 1024
-    columns), with a partial last block, then the same call in place."""
+    columns), with a partial last block (1001 and 13001 rows end in a one-row block), then
+    the same call in place."""
     say(f"softmax short rows={rows} cols={cols} {idt}->{odt}")
     x = inp(orc, (rows, cols), 37, cols, idt, std=3.0)
     xd = to_dev(x, idt)
