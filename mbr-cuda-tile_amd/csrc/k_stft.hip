@@ -410,6 +410,55 @@ __device__ __forceinline__ int stage_span(const StftArgs& a, float* stage, uint3
     return 0;
 }
 
+// The staged prologue when the workgroup's span lies inside its signal and the window and
+// signal are aligned (the common case): the window, the twiddles and the span (KS float4
+// per thread, indices clamped to the span's last whole vector) are all loaded before the
+// first LDS write, so the workgroup pays one memory round trip instead of one per load
+// group.  The span's last partial vector (1..3 samples) is read by thread 0.  Returns the
+// span's offset in the staging area, as stage_span.
+template <int NT, int KS>
+__device__ __forceinline__ int stage_all(const StftArgs& a, float* stage, float2* tw, uint32_t b, int s, int span) {
+    const int tid = threadIdx.x;
+    const int64_t base = (int64_t)b * a.L + s, end = base + span;
+    const int64_t a4 = base & ~int64_t(3);
+    const int xoff = (int)(base - a4), n4 = (xoff + span + 3) >> 2;
+    const int nfull = (int)((end - a4) >> 2);  // vectors wholly inside the span (>= 1)
+    constexpr int kW = kN / 2 / NT, kT = kTwHalf / NT;
+    float2 wv[kW], tv[kT];
+    float4 xv[KS];
+    const float2* tsrc = reinterpret_cast<const float2*>(kTwiddles.v);
+#pragma unroll
+    for (int k = 0; k < kW; ++k) wv[k] = reinterpret_cast<const float2*>(a.w)[tid + k * NT];
+#pragma unroll
+    for (int k = 0; k < kT; ++k) tv[k] = tsrc[tid + k * NT];
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + a4);
+#pragma unroll
+    for (int k = 0; k < KS; ++k) xv[k] = x4[min(tid + k * NT, nfull - 1)];
+    float tail[3] = {0.0f, 0.0f, 0.0f};
+    if (tid == 0 && n4 > nfull) {
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {
+            const int64_t q = a4 + 4 * (int64_t)nfull + e;
+            tail[e] = q < end ? a.x[q] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kW; ++k) reinterpret_cast<float2*>(stage)[tid + k * NT] = wv[k];
+#pragma unroll
+    for (int k = 0; k < kT; ++k) tw[tw_pos(tid + k * NT)] = tv[k];
+    float* xst = stage + kN;
+    // unconditional writes (threads past the span rewrite its last whole vector with the
+    // same bytes): a predicated write would let the compiler sink each load into its branch
+    // and wait for it there, one round trip per load
+#pragma unroll
+    for (int k = 0; k < KS; ++k) reinterpret_cast<float4*>(xst)[min(tid + k * NT, nfull - 1)] = xv[k];
+    if (tid == 0 && n4 > nfull) {
+#pragma unroll
+        for (int e = 0; e < 3; ++e) xst[4 * nfull + e] = tail[e];
+    }
+    return xoff;
+}
+
 template <int TF>
 __global__ __launch_bounds__(64 * TF) void stft_kernel(StftArgs a) {
     constexpr int NT = 64 * TF;
@@ -428,8 +477,14 @@ __global__ __launch_bounds__(64 * TF) void stft_kernel(StftArgs a) {
         // from HBM once, coalesced, into the frame slots, and each wave takes its frame there
         const int s = (int)t0 * a.hop - a.offset;
         float* stage = reinterpret_cast<float*>(lds);
-        const int xoff = stage_span<NT>(a, stage, b, s, (nf - 1) * a.hop + kN);
-        load_twiddles<NT>(tw);
+        const int span = (nf - 1) * a.hop + kN;
+        int xoff;
+        if (a.wvec && a.xvec && s >= 0 && s + span <= a.L && span + 3 <= 4 * 4 * NT) {
+            xoff = stage_all<NT, 4>(a, stage, tw, b, s, span);
+        } else {
+            xoff = stage_span<NT>(a, stage, b, s, span);
+            load_twiddles<NT>(tw);
+        }
         __syncthreads();
         if (live) {
             const float* xs = stage + kN + xoff + wave * a.hop;
@@ -529,6 +584,11 @@ __global__ __launch_bounds__(64 * TF) void istft_block_kernel(IstftBlockArgs a) 
     fdivmod(blk, a.ntb, b, tb);
     const uint32_t t0 = tb * TF;
     const uint32_t nf = min((uint32_t)TF, a.T - t0);
+    // the twiddle loads go out with the spectrum's, one memory round trip for both
+    constexpr int kT = kTwHalf / NT;
+    float2 tv[kT];
+#pragma unroll
+    for (int k = 0; k < kT; ++k) tv[k] = reinterpret_cast<const float2*>(kTwiddles.v)[threadIdx.x + k * NT];
     {
         // transposed spectrum load: thread -> (frame tl, bins fr + 64 k, k = 0..15, and bin
         // 1024 for fr = 0); all 16 (17) loads are in flight before the first LDS write
@@ -548,7 +608,8 @@ __global__ __launch_bounds__(64 * TF) void istft_block_kernel(IstftBlockArgs a) 
             if (fr == 0) slot[pad16(kN / 2)] = make_float2(X[16].x * a.spec_scale, X[16].y * a.spec_scale);
         }
     }
-    load_twiddles<NT>(tw);
+#pragma unroll
+    for (int k = 0; k < kT; ++k) tw[tw_pos(threadIdx.x + k * NT)] = tv[k];
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if ((uint32_t)wave < nf) {
