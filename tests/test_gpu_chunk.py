@@ -20,6 +20,8 @@ pytestmark = pytest.mark.gpu
     (3, 18601, [(0, 4000), (3200, 4000), (6400, 4000), (9600, 4000), (12800, 4000), (16000, 2601)]),  # scalar path
     (8, 1058400, [(0, 352800), (264600, 352800), (529200, 352800), (705600, 352800)]),  # 8 channels, 8 s chunks
     (1, 7, [(0, 3), (2, 5), (6, 1)]),
+    (12, 8000, [(0, 4000), (2000, 4000), (4000, 4000)]),  # float4, 4 channels per thread, 3 groups
+    (5, 8000, [(0, 4000), (4000, 4000)]),  # float4, 1 channel per thread, 5 groups
 ])
 def test_chunk_accumulate_and_normalize_bitexact(orc, dev, C, L, calls):
     say(f"chunk accumulate C={C} L={L} calls={len(calls)}")
