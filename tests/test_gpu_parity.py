@@ -874,10 +874,13 @@ def test_attention_bnhd_fusions(orc, dev, B, N, H, rot, gate, odt, tdt):
         assert_close(to_host(fused, odt), gref, odt, "attention_bnhd gate merge")
 
 
-def test_attention_bnhd_p_bf16_fusion(orc, dev):
+@pytest.mark.parametrize("fast", [False, True])
+def test_attention_bnhd_p_bf16_fusion(orc, dev, fast):
     """The reference's split-contig q-rotary time attention with the gate, in the
-    reference's P arithmetic: bit for bit rotary -> attention(P-bf16) -> gate merge."""
-    say("attention_bnhd P-bf16 rot+gate")
+    reference's P arithmetic (and in the fast bf16-P mode): bit for bit rotary ->
+    attention -> gate merge."""
+    say(f"attention_bnhd P-bf16 rot+gate fast={fast}")
+    pm = mbrt.ATTN_P_BF16_FAST if fast else mbrt.ATTN_P_BF16
     B, N, H = 2, 801, 8
     qkv = to_dev(inp(orc, (B, N, 3 * H * 64), 0x4D425200B5, 0, BF16), BF16)
     v5 = qkv.view(B, N, 3, H, 64)
@@ -885,17 +888,18 @@ def test_attention_bnhd_p_bf16_fusion(orc, dev):
     cos_h, sin_h = orc.rotary_tables(N, 64)
     cos, sin = to_dev(cos_h, F32), to_dev(sin_h, F32)
     g = to_dev(inp(orc, (B, N, H), 0x4D425200B6, 0, BF16, std=2.0), BF16)
-    fused = mbrt.attention_bnhd(q, k, v, cos=cos, sin=sin, gate=g, p_bf16=True)
+    fused = mbrt.attention_bnhd(q, k, v, cos=cos, sin=sin, gate=g, p_precision=pm)
     qc, kc, vc = (t.permute(0, 2, 1, 3).contiguous().view(B * H, N, 64) for t in (q, k, v))
     mbrt.rotary_(qc, None, cos, sin)
     att = empty((B, H, N, 64), BF16)
-    mbrt.attention(qc, kc, vc, att.view(B * H, N, 64), 0.0, p_bf16=True)
+    mbrt.attention(qc, kc, vc, att.view(B * H, N, 64), 0.0, p_precision=pm)
     sep = empty((B, N, H * 64), BF16)
     mbrt.gate_merge(att, g, sep)
     torch.cuda.synchronize()
     assert_bitexact(to_host(fused, BF16), to_host(sep, BF16), "attention_bnhd P-bf16 = separate ops")
     qh, kh, vh = (to_host(t[:2], BF16) for t in (qc, kc, vc))
-    _assert_ref_p(orc, to_host(att.view(B * H, N, 64)[:2], BF16), qh, kh, vh, BF16, 0.0, "bnhd P-bf16 attention")
+    _assert_ref_p(orc, to_host(att.view(B * H, N, 64)[:2], BF16), qh, kh, vh, BF16, 0.0, "bnhd P-bf16 attention",
+                  fast=fast)
 
 
 @pytest.mark.parametrize("gdt,logit,odt", [(F32, True, BF16), (F16, True, F32), (BF16, False, BF16),
