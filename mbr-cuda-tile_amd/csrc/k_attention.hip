@@ -41,6 +41,9 @@ constexpr int kQWave = 16;     // queries per wave
 constexpr int kWaves = 4;
 constexpr int kQBlock = kQWave * kWaves;
 constexpr float kLazy = 8.0f;  // log2 units the running max may outgrow the exponent reference
+// Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format, no swizzle,
+// no stride): loads of byte offset o < num_records read base + o.
+constexpr int kBufferDword3 = 0x00020000;
 #ifndef MBRT_ATTN_WPE
 #define MBRT_ATTN_WPE 4  // waves per SIMD the register budget is sized for (4: at most 128 VGPRs)
 #endif
@@ -229,9 +232,30 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBR
     // a tile, 8 per instruction: lane i -> key 16w + 8u + i/8, stored chunk i % 8, which
     // holds logical chunk (i % 8) ^ (i / 8).  Keys past N load a clamped row (masked later).
     // Element offsets within one (b, h) fit 32 bits (n_k * 64 < 2^31 is checked on the host).
+    // A whole tile (no key past N) loads through buffer resources of this head's K and V
+    // rows: the tile's first row is a scalar offset (kt rows in bytes) and each lane's two
+    // chunks fixed 32-bit offsets from it, so a tile's addresses cost no vector
+    // instructions.  The rows of one head span < 2^32 bytes (checked on the host), so the
+    // offsets and their sums stay below the descriptors' 2^32 - 1 records.
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, -1, kBufferDword3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, -1, kBufferDword3);
+    uint32_t loff[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        loff[u] = 2u * ((uint32_t)(16 * w + 8 * u + (lane >> 3)) * (uint32_t)a.kv_rs + 8u * ((lane & 7) ^ (lane >> 3)));
     auto load_tile = [&](int kt, int buf) {
         __bf16* kd = buf ? k1 : k0;
         __bf16* vd = buf ? v1 : v0;
+        if (kt + kKeys <= a.nk) {
+            const int soff = (int)(2u * (uint32_t)kt * (uint32_t)a.kv_rs);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int r0 = 16 * w + 8 * u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)&kd[r0 * kHeadDim], 16, loff[u], soff, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)&vd[r0 * kHeadDim], 16, loff[u], soff, 0, 0);
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int r0 = 16 * w + 8 * u, key = r0 + (lane >> 3);
