@@ -656,7 +656,10 @@ def test_zero_dc(orc, dev):
                                       (2, 801, 801), (2, 37, 200), (2, 200, 37),
                                       # 128-query workgroups whose last one holds 1 or 33 queries (its
                                       # other waves only load and sync), and one query or one key
-                                      (2, 129, 129), (1, 161, 70), (2, 1, 801), (2, 801, 1)])
+                                      (2, 129, 129), (1, 161, 70), (2, 1, 801), (2, 801, 1),
+                                      # keys in whole 64-key tiles only (every tile through the
+                                      # buffer-resource loads, the last one too)
+                                      (2, 100, 128), (1, 70, 768)])
 @pytest.mark.parametrize("odt", [BF16, F32])
 def test_attention_shapes(orc, dev, BH, nq, nk, odt):
     say(f"attention BH={BH} nq={nq} nk={nk} out={odt}")
@@ -713,7 +716,7 @@ def _assert_ref_p(orc, y, q, k, v, odt, scale, what, fast=False):
 
 
 @pytest.mark.parametrize("BH,nq,nk", [(3, 1, 1), (2, 65, 65), (2, 801, 801), (2, 37, 200), (2, 129, 129),
-                                      (2, 801, 1), (1, 161, 70)])
+                                      (2, 801, 1), (1, 161, 70), (2, 64, 64), (2, 96, 128)])
 @pytest.mark.parametrize("odt", [BF16, F32])
 def test_attention_p_bf16(orc, dev, BH, nq, nk, odt):
     say(f"attention P-bf16 BH={BH} nq={nq} nk={nk} out={odt}")
@@ -744,7 +747,7 @@ def test_attention_p_bf16_known_answer(orc, dev):
 
 
 @pytest.mark.parametrize("BH,nq,nk", [(3, 1, 1), (2, 65, 65), (2, 801, 801), (2, 37, 200), (2, 129, 129),
-                                      (2, 801, 1), (1, 161, 70), (2, 300, 700)])
+                                      (2, 801, 1), (1, 161, 70), (2, 300, 700), (2, 64, 64), (2, 96, 128)])
 @pytest.mark.parametrize("odt", [BF16, F32])
 def test_attention_p_bf16_fast(orc, dev, BH, nq, nk, odt):
     say(f"attention P-bf16 fast BH={BH} nq={nq} nk={nk} out={odt}")
