@@ -204,6 +204,9 @@ __device__ __forceinline__ void fdivmod(uint32_t n, const FastDiv& f, uint32_t& 
 // at most N are outstanding completes everything issued before the last N.
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void global_void;
+// Cache-policy operand of those builtins: the non-temporal (nt) bit of gfx940-family
+// memory instructions, as __builtin_nontemporal_load sets it on ordinary loads.
+constexpr int kCpolNt = 2;
 typedef __attribute__((address_space(4))) const int32_t const_i32;
 
 // s_waitcnt vmcnt(N) with expcnt and lgkmcnt left free (gfx9 encoding: vmcnt in bits 3:0

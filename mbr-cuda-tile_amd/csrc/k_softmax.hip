@@ -112,6 +112,24 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
     const int nel = nrows * a.cols;
     const int64_t ebase = row0 * a.cols;
     const int nvi = nel / VI;
+    // When LDS holds the span's raw bytes (f32 -> f32, and 2-byte spans kept 2-byte), the
+    // span goes straight from HBM into LDS: lane i of wave w's k-th load writes vector
+    // 256 k + 64 w + i at its place in buf (global_load_lds_dwordx4, non-temporal when the
+    // kernel's loads are).  Time f32 428.0-428.4 -> 425.1-425.3 us against the same loads
+    // through registers.
+    constexpr bool kDma = MBRT_SM_DMA != 0 && (K16 || (IDT == F32 && ODT == F32));
+    if constexpr (kDma) {
+        const char* src = reinterpret_cast<const char*>(a.in) + ebase * DtSize<IDT>::value;
+        const int w = tid / 64;
+#pragma unroll
+        for (int k = 0; k < KI; ++k) {
+            const int v = tid + kThreads * k;
+            if (v < nvi)
+                __builtin_amdgcn_global_load_lds((global_void*)(src + (int64_t)v * 16),
+                                                 (lds_void*)&buf[(kThreads * k + 64 * w) * VI], 16, 0,
+                                                 (NT & 1) != 0 ? kCpolNt : 0);
+        }
+    } else {
     Vec<IDT, VI> iv[KI];
 #pragma unroll
     for (int k = 0; k < KI; ++k) iv[k].template load<NT>(a.in, ebase + (int64_t)min(tid + kThreads * k, nvi - 1) * VI);
@@ -128,6 +146,7 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
                 for (int i = 0; i < VI; ++i) buf[v * VI + i] = f[i];
             }
         }
+    }
     }
     __syncthreads();
     auto get = [&](int e) -> float {

@@ -79,6 +79,9 @@
 #ifndef MBRT_SM_SHORT_BYTES
 #define MBRT_SM_SHORT_BYTES 6144  // staged softmax rows of 33..64: below this many input bytes per 32 rows, 64-row blocks
 #endif
+#ifndef MBRT_SM_DMA
+#define MBRT_SM_DMA 1  // staged softmax: raw spans loaded straight into LDS (direct-to-LDS loads)
+#endif
 #ifndef MBRT_SM_SHORT_RPG
 #define MBRT_SM_SHORT_RPG 2  // rows per lane group in those blocks
 #endif
