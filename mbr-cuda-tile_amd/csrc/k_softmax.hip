@@ -81,8 +81,9 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
 // b*RB*cols.  The launcher only picks this kernel when
 // that span is a whole number of 16-byte vectors for the input and the output dtype, both
 // pointers are 16-byte aligned and rows*cols fills whole vectors, so every vector lies in
-// one block's span.  Phase 1 loads the span (clamped vector indices, predicated LDS
-// writes), phase 2 is the same register-resident group softmax as above but fed from LDS,
+// one block's span.  Phase 1 loads the span into LDS (straight from HBM, or through
+// registers where it changes dtype), phase 2 is the same register-resident group softmax
+// as above but fed from LDS,
 // writing the probabilities back over their inputs, phase 3 stores the span.  In-place
 // calls are safe: the whole span is in LDS before its first store.
 template <int IDT, int ODT, int G, int NM, int RPG>
@@ -130,23 +131,26 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
                                                  (NT & 1) != 0 ? kCpolNt : 0);
         }
     } else {
-    Vec<IDT, VI> iv[KI];
+        // through registers: the loads are all issued first (vector indices clamped into
+        // the span), then converted and written to LDS
+        Vec<IDT, VI> iv[KI];
 #pragma unroll
-    for (int k = 0; k < KI; ++k) iv[k].template load<NT>(a.in, ebase + (int64_t)min(tid + kThreads * k, nvi - 1) * VI);
+        for (int k = 0; k < KI; ++k)
+            iv[k].template load<NT>(a.in, ebase + (int64_t)min(tid + kThreads * k, nvi - 1) * VI);
 #pragma unroll
-    for (int k = 0; k < KI; ++k) {
-        const int v = tid + kThreads * k;
-        if (v < nvi) {
-            if constexpr (K16) {
-                *reinterpret_cast<u32x4*>(&buf[v * VI]) = u32x4{iv[k].w[0], iv[k].w[1], iv[k].w[2], iv[k].w[3]};
-            } else {
-                float f[VI];
-                iv[k].to_f32(f);
+        for (int k = 0; k < KI; ++k) {
+            const int v = tid + kThreads * k;
+            if (v < nvi) {
+                if constexpr (K16) {
+                    *reinterpret_cast<u32x4*>(&buf[v * VI]) = u32x4{iv[k].w[0], iv[k].w[1], iv[k].w[2], iv[k].w[3]};
+                } else {
+                    float f[VI];
+                    iv[k].to_f32(f);
 #pragma unroll
-                for (int i = 0; i < VI; ++i) buf[v * VI + i] = f[i];
+                    for (int i = 0; i < VI; ++i) buf[v * VI + i] = f[i];
+                }
             }
         }
-    }
     }
     __syncthreads();
     auto get = [&](int e) -> float {
