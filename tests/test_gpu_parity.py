@@ -456,6 +456,35 @@ def test_softmax_short_rows(orc, dev, rows, cols, idt, odt):
         assert_bitexact(to_host(xd, odt), to_host(y, odt), "softmax short in place")
 
 
+@pytest.mark.parametrize("rows,cols", [(96, 801), (96, 60), (96, 16), (23, 801), (23, 60), (5, 3000)])
+@pytest.mark.parametrize("dt", [F32, BF16])
+def test_softmax_special_values(orc, dev, rows, cols, dt):
+    """Masked scores on every softmax path (LDS-staged long and short rows, the unaligned
+    rows kernel, the long-row loop): -inf entries get probability 0 and the row still sums
+    to 1, a fully masked row and a row holding +inf become NaN, as in the oracle."""
+    say(f"softmax special values rows={rows} cols={cols} dt={dt}")
+    x = orc.to_f32(inp(orc, (rows, cols), 41, cols, dt, std=3.0), dt).copy()
+    x[1, ::7] = -np.inf
+    x[2, :] = -np.inf
+    x[3, cols // 2] = np.inf
+    x[4, : cols - 1] = -np.inf  # one live element: probability 1
+    x = orc.from_f32(x, dt)
+    xd = to_dev(x, dt)
+    y = empty((rows, cols), dt)
+    mbrt.softmax(xd, y, 0.5)
+    torch.cuda.synchronize()
+    want = orc.softmax(x, dt, dt, 0.5)
+    got = to_host(y, dt)
+    assert_close(got, want, dt, "softmax special values")
+    g = orc.to_f32(got, dt)
+    assert np.all(g[1, ::7] == 0.0) and abs(float(g[1].sum(dtype=np.float64)) - 1.0) < 1e-2
+    assert np.isnan(g[2]).all() and np.isnan(g[3]).all()
+    assert g[4, cols - 1] == 1.0
+    mbrt.softmax(xd, xd, 0.5)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(xd, dt), got, "softmax special values in place")
+
+
 # ---- rotary --------------------------------------------------------------------------------
 
 def test_rotary_bl4a_full(orc, dev):
