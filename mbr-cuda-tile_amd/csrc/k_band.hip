@@ -128,7 +128,17 @@ __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
 // loads (row indices and frames are clamped, never skipped).  vmcnt retires in issue
 // order, so "at most kLPT outstanding" means every op before the newest tile's loads has
 // completed, in particular the loads of the tile about to be read.
+//
+// Line-aligned stores (MBRT_BAND_GALIGN).  An output row (one frame, J band-bins) starts
+// at (b T + t) J complex values, so with J = 3958 most 64-value runs start inside a
+// 128-byte line and share their first and last lines with the neighbouring tiles; those
+// split lines cost about 8 % (measured with a padded row pitch).  So tile k owns, in frame
+// row t, the band-bins [64 k - ph(t), 64 k + 64 - ph(t)), ph(t) the row's offset into its
+// line (in complex values, < 16): every run is whole lines.  Its LDS buffer holds the 16
+// band-bins before 64 k as well (80 rows), and the tile grid has one more band-bin tile.
 constexpr int kGTJ = 64;  // band-bins per tile: one per lane when storing
+constexpr int kGShift = MBRT_BAND_GALIGN ? 16 : 0;  // extra rows before a tile's first band-bin
+constexpr int kGRows = kGTJ + kGShift;              // LDS rows per tile
 
 struct GatherPipeArgs {
     const float* stft;
@@ -138,6 +148,7 @@ struct GatherPipeArgs {
     int32_t bft2;                 // F * T * 2: floats per batch of stft (B * F * T * 2 < 2^31)
     FastDiv tiles_j, tiles_t;     // tile grid: band-bin tiles fastest, then frames, then batch
     uint32_t tiles;
+    uint32_t oph;                 // (output address / bytes per complex value) % 16
 };
 
 // Barrier for data that arrived by direct-to-LDS loads: the caller has waited (vmcnt) for
@@ -151,6 +162,23 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// 16 ds_read_b64: v[q + 4 m] from LDS byte address a[q] + 128 m (q, m < 4), completed
+// before the statement ends; one asm block for the reason given at lds_read_b64_n.
+__device__ __forceinline__ void lds_read_b64_4x4(const uint32_t (&a)[4], f32x2 (&v)[16]) {
+#define MBRT_DSR4(i, q, m) "ds_read_b64 %" #i ", %" #q " offset:" #m "\n\t"
+    asm volatile(MBRT_DSR4(0, 16, 0) MBRT_DSR4(1, 17, 0) MBRT_DSR4(2, 18, 0) MBRT_DSR4(3, 19, 0)
+                 MBRT_DSR4(4, 16, 128) MBRT_DSR4(5, 17, 128) MBRT_DSR4(6, 18, 128) MBRT_DSR4(7, 19, 128)
+                 MBRT_DSR4(8, 16, 256) MBRT_DSR4(9, 17, 256) MBRT_DSR4(10, 18, 256) MBRT_DSR4(11, 19, 256)
+                 MBRT_DSR4(12, 16, 384) MBRT_DSR4(13, 17, 384) MBRT_DSR4(14, 18, 384) MBRT_DSR4(15, 19, 384)
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+                   "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]), "=&v"(v[12]), "=&v"(v[13]),
+                   "=&v"(v[14]), "=&v"(v[15])
+                 : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3])
+                 : "memory");
+#undef MBRT_DSR4
+}
+
 // Freq of a row from its raw index (int32, or the low/high words of an int64), clamped
 // into [0, F): an index outside the tensor reads the nearest valid row.
 __device__ __forceinline__ int32_t clamp_freq(int32_t lo, int32_t hi, int32_t F) {
@@ -161,16 +189,18 @@ __device__ __forceinline__ int32_t clamp_freq(int32_t lo, int32_t hi, int32_t F)
 template <int ODT, bool I64, int NW, int TT>
 __global__ __launch_bounds__(64 * NW) void band_gather_pipe_kernel(GatherPipeArgs a) {
     constexpr int kRowF = 2 * TT + 2;    // floats per LDS row: TT complex values + 8 B of padding
-    constexpr int kRPW = kGTJ / NW;      // rows a wave loads per tile
+    constexpr int kRPW = kGRows / NW;    // rows a wave loads per tile
     constexpr int kIPR = TT / 32;        // direct loads per row
     constexpr int kLPT = kRPW * kIPR;    // direct loads per wave per tile
     constexpr int kFPW = TT / NW;        // frames a wave stores per tile
-    static_assert(TT % 32 == 0 && kGTJ % NW == 0 && TT % NW == 0 && kLPT < 64, "tile shape");
+    static_assert(TT % 32 == 0 && kGRows % NW == 0 && TT % NW == 0 && kLPT < 64, "tile shape");
+    // the frames a wave stores, w + NW r, have at most 4 line offsets (period 4 in r)
+    static_assert(kGShift == 0 || (NW == 4 && kFPW == 16), "aligned stores: 4 waves, 64-frame tiles");
     // three separate LDS objects: the compiler can tell the loads in flight into one buffer
     // from the reads of another
-    __shared__ float buf0[kGTJ * kRowF];
-    __shared__ float buf1[kGTJ * kRowF];
-    __shared__ float buf2[kGTJ * kRowF];
+    __shared__ float buf0[kGRows * kRowF];
+    __shared__ float buf1[kGRows * kRowF];
+    __shared__ float buf2[kGRows * kRowF];
     const int lane = threadIdx.x % 64;
     const int w = wave_id();
     const int64_t n = a.tiles, G = gridDim.x;
@@ -192,10 +222,10 @@ __global__ __launch_bounds__(64 * NW) void band_gather_pipe_kernel(GatherPipeArg
     // J - 1); they are clamped where used, so the loads of a tile are all in flight at once
     int32_t flo[kRPW], fhi[kRPW];
     auto fetch_rows = [&](const Tile& t) {
-        const int32_t jb = t.j0 + w * kRPW;
+        const int32_t jb = t.j0 - kGShift + w * kRPW;
 #pragma unroll
         for (int q = 0; q < kRPW; ++q) {
-            const int32_t j = min(jb + q, a.J - 1);
+            const int32_t j = min(max(jb + q, 0), a.J - 1);
             if constexpr (I64) {
                 flo[q] = scalar_load_i32(a.idx, 2 * (int64_t)j);
                 fhi[q] = scalar_load_i32(a.idx, 2 * (int64_t)j + 1);
@@ -227,19 +257,46 @@ __global__ __launch_bounds__(64 * NW) void band_gather_pipe_kernel(GatherPipeArg
     // (element offsets fit 32 bits: B * T * J * 2 < 2^31 is checked on the host)
     auto store = [&](const Tile& t, const float* buf) {
         f32x2 v[kFPW];
-        lds_read_b64_n<kFPW, 0, 8 * NW>(lds_addr(buf) + (uint32_t)(lane * kRowF + 2 * w) * 4, v);
-        const int32_t j = t.j0 + lane;
-        if (j >= a.J) return;
-        int32_t o = (t.b * a.T + t.t0 + w) * a.J + j;
-        const int32_t step_o = NW * a.J;
-        if (t.t0 + TT <= a.T) {
+        if constexpr (kGShift == 0) {
+            lds_read_b64_n<kFPW, 0, 8 * NW>(lds_addr(buf) + (uint32_t)(lane * kRowF + 2 * w) * 4, v);
+            const int32_t j = t.j0 + lane;
+            if (j >= a.J) return;
+            int32_t o = (t.b * a.T + t.t0 + w) * a.J + j;
+            const int32_t step_o = NW * a.J;
+            if (t.t0 + TT <= a.T) {
 #pragma unroll
-            for (int r = 0; r < kFPW; ++r, o += step_o) store_complex<ODT>(a.out, o, v[r]);
+                for (int r = 0; r < kFPW; ++r, o += step_o) store_complex<ODT>(a.out, o, v[r]);
+            } else {
+                const int nv = (a.T - t.t0 - w + NW - 1) / NW;  // frames of this wave inside T
+#pragma unroll
+                for (int r = 0; r < kFPW; ++r, o += step_o)
+                    if (r < nv) store_complex<ODT>(a.out, o, v[r]);
+            }
         } else {
-            const int nv = (a.T - t.t0 - w + NW - 1) / NW;  // frames of this wave inside T
+            // frame w + 4 (q + 4 m) of the tile: its row's line offset ph_q depends on q only
+            // (4 J (q + 4 m) = 4 J q mod 16); lane l writes band-bin j0 - ph_q + l, which
+            // is LDS row l + 16 - ph_q
+            int32_t jq[4], oq[4];
+            uint32_t aq[4];
 #pragma unroll
-            for (int r = 0; r < kFPW; ++r, o += step_o)
-                if (r < nv) store_complex<ODT>(a.out, o, v[r]);
+            for (int q = 0; q < 4; ++q) {
+                const int32_t row0 = (t.b * a.T + t.t0 + w + 4 * q) * a.J;  // first value of the frame row
+                const int32_t ph = (int32_t)(((uint32_t)(row0 + t.j0) + a.oph) & 15u);
+                jq[q] = t.j0 - ph + lane;
+                oq[q] = row0 + jq[q];
+                aq[q] = lds_addr(buf) + (uint32_t)((lane + kGShift - ph) * kRowF + 2 * (w + 4 * q)) * 4;
+            }
+            lds_read_b64_4x4(aq, v);
+            const int32_t step_o = 16 * a.J;  // 16 frames
+            const int nv = t.t0 + TT <= a.T ? kFPW : (a.T - t.t0 - w + NW - 1) / NW;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (jq[q] >= 0 && jq[q] < a.J) {
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        if (q + 4 * m < nv) store_complex<ODT>(a.out, oq[q] + m * step_o, v[q + 4 * m]);
+                }
+            }
         }
     };
     // Tile k of this block is p0 + k G and lives in buffer k % 3.  A steady step k reads
@@ -357,7 +414,9 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     const int64_t mbase = (int64_t)b * a.T;
     for (int c0 = e_begin; c0 < e_end; c0 += kME) {
         const int c1 = min(c0 + kME, e_end);
-        const int j = min(max(ld_idx<I64>(a.ind, min(c0 + lane, c1 - 1)), 0), a.J - 1);
+        // entry and band-bin clamped into ind[0, J) and [0, J): offsets past J read in bounds
+        const int ei = min(max(min(c0 + lane, c1 - 1), 0), a.J - 1);
+        const int j = min(max(ld_idx<I64>(a.ind, ei), 0), a.J - 1);
         f32x2 mv[kR];
 #pragma unroll
         for (int r = 0; r < kR; ++r)
@@ -438,7 +497,10 @@ int mbrt_band_gather(const float* stft, const void* freq_indices, int index_dtyp
         g.T = (int32_t)frames;
         g.J = (int32_t)n_band_freqs;
         g.bft2 = (int32_t)(total_freq * frames * 2);
-        const int64_t tj = ceil_div(n_band_freqs, kGTJ), tt = ceil_div(frames, TT), tiles = tj * tt * B;
+        // aligned stores shift a tile's band-bins down by up to 15: one more tile covers the end
+        const int64_t tj = ceil_div(n_band_freqs + (kGShift ? 15 : 0), kGTJ), tt = ceil_div(frames, TT);
+        const int64_t tiles = tj * tt * B;
+        g.oph = (uint32_t)((reinterpret_cast<uintptr_t>(out) / (out_dtype == F32 ? 8 : 4)) % 16);
         g.tiles_j = make_fastdiv((uint32_t)tj);
         g.tiles_t = make_fastdiv((uint32_t)tt);
         g.tiles = (uint32_t)tiles;
@@ -494,7 +556,9 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
     a.mask[0] = masks[0];
     a.mask[1] = num_stems == 2 ? masks[1] : masks[0];
     a.off = csr_offsets;
-    a.ind = csr_indices;
+    // with no band freqs (csr_indices may then be NULL) the clamped index loads of offsets
+    // that are not all zero read the offsets instead
+    a.ind = n_band_freqs > 0 ? csr_indices : csr_offsets;
     a.cnt = counts;
     a.out = out;
     a.cdt = counts_dtype;

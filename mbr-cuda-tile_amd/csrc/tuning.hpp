@@ -58,6 +58,9 @@
 #ifndef MBRT_BAND_GNW
 #define MBRT_BAND_GNW 4  // pipelined band gather: waves per block
 #endif
+#ifndef MBRT_BAND_GALIGN
+#define MBRT_BAND_GALIGN 1  // pipelined band gather: output runs start on 128-byte lines (1) or at the tile (0)
+#endif
 #ifndef MBRT_BAND_GBPC
 #define MBRT_BAND_GBPC 1  // pipelined band gather: persistent blocks per CU
 #endif
