@@ -134,8 +134,9 @@ __global__ __launch_bounds__(kThreads) void band_gather_kernel(GatherArgs a) {
 // 128-byte line and share their first and last lines with the neighbouring tiles; those
 // split lines cost about 8 % (measured with a padded row pitch).  So tile k owns, in frame
 // row t, the band-bins [64 k - ph(t), 64 k + 64 - ph(t)), ph(t) the row's offset into its
-// line (in complex values, < 16): every run is whole lines.  Its LDS buffer holds the 16
-// band-bins before 64 k as well (80 rows), and the tile grid has one more band-bin tile.
+// line (in complex values, < 16): every run of an f32 output is whole lines (a 2-byte
+// output's runs start on 64-byte boundaries).  Its LDS buffer holds the 16 band-bins
+// before 64 k as well (80 rows), and the tile grid has one more band-bin tile.
 constexpr int kGTJ = 64;  // band-bins per tile: one per lane when storing
 constexpr int kGShift = MBRT_BAND_GALIGN ? 16 : 0;  // extra rows before a tile's first band-bin
 constexpr int kGRows = kGTJ + kGShift;              // LDS rows per tile
