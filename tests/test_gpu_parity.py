@@ -582,6 +582,29 @@ def test_band_gather_shapes(orc, dev, B, F, T, J, idt, odt, seed):
     assert_bitexact(to_host(out, odt), orc.band_gather(stft, idx, odt, B, F, T), "gather")
 
 
+# The gather starts every output run on a line of the output row, which depends on the
+# output's address: outputs placed 1..15 complex values past an aligned address, with
+# guard values around them that must stay untouched.
+@pytest.mark.parametrize("B,F,T,J,idt,odt", [(2, 2050, 70, 3958, I32, F32), (1, 300, 33, 100, I64, F32),
+                                             (3, 70, 5, 17, I32, BF16), (1, 513, 130, 200, I32, F16)])
+@pytest.mark.parametrize("shift", [1, 3, 8, 15])
+def test_band_gather_output_offsets(orc, dev, B, F, T, J, idt, odt, shift):
+    say(f"band gather into an output {shift} complex values past alignment B={B} T={T} J={J} out={odt}")
+    rng = np.random.default_rng(shift * 131 + J)
+    idx = rng.integers(0, F, size=J).astype(np.int64 if idt == I64 else np.int32)
+    stft = inp(orc, (B, F, T, 2), 70 + shift, 0)
+    n = B * T * J * 2  # output scalars
+    buf = empty((n + 64,), odt)
+    buf.fill_(-3.0)
+    out = buf[2 * shift: 2 * shift + n].view(B, T, J * 2)
+    mbrt.band_gather(to_dev(stft, F32), to_dev(idx, idt), out)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(out, odt), orc.band_gather(stft, idx, odt, B, F, T), "gather at an offset")
+    host = to_host(buf, odt)
+    guard = to_host(torch.full((1,), -3.0, dtype=buf.dtype, device="cuda"), odt)[0]
+    assert (host[:2 * shift] == guard).all() and (host[2 * shift + n:] == guard).all(), "gather wrote outside its output"
+
+
 @pytest.mark.parametrize("idt", [I32, I64])
 def test_band_gather_out_of_range_indices_clamp(orc, dev, idt):
     say(f"band gather with out-of-range indices idx={idt}")
