@@ -692,6 +692,41 @@ def test_band_merge_many_bands_per_freq(orc, dev):
     assert_close(to_host(out, F32), ref, F32, "merge chunked", den=merge_den(orc, stft, [mask], mbd, B, F, T, C))
 
 
+def test_band_merge_freqs_without_bands(orc, dev):
+    """Freqs that no band covers (count 0: nothing to sum, divided by max(count, 1e-8))
+    give 0; with no band freqs at all (empty CSR, no index array) every output is 0."""
+    say("band merge with uncovered freqs and with no band freqs")
+    B, F, T, C = 2, 40, 70, 2
+    fi = np.concatenate([np.arange(4, 20), np.arange(12, 30)]).astype(np.int32)  # freqs 0-3 and 30-39 uncovered
+    J = fi.size
+    by = [[] for _ in range(F)]
+    for j, f in enumerate(fi):
+        by[f].append(j)
+    off = np.zeros(F + 1, np.int32)
+    off[1:] = np.cumsum([len(b) for b in by])
+    ind = np.array([j for b in by for j in b], np.int32)
+    cnt = np.array([len(b) for b in by], np.float32)
+    stft = inp(orc, (B, F, T, 2), 45, 0)
+    mask = inp(orc, (B, T, J * 2), 45, 1)
+    out = empty((B * C, F // C, T, 2), F32)
+    mbrt.band_mask_merge(to_dev(stft, F32), [to_dev(mask, F32)], to_dev(off, I32), to_dev(ind, I32), to_dev(cnt, F32),
+                         out, C)
+    torch.cuda.synchronize()
+    ref = orc.band_mask_merge(stft, [mask.reshape(B, T, J, 2)], F32, off, ind, cnt, F32, F32, B, F, T, C)
+    got = to_host(out, F32)
+    mbd = dict(bands_per_freq=cnt.astype(np.int32), csr_offsets=off, csr_indices=ind)
+    assert_close(got, ref, F32, "merge with uncovered freqs", den=merge_den(orc, stft, [mask], mbd, B, F, T, C))
+    per_freq = got.reshape(B, C, F // C, T, 2).transpose(0, 2, 1, 3, 4).reshape(B, F, T, 2)
+    assert (per_freq[:, :4] == 0).all() and (per_freq[:, 30:] == 0).all()
+    # no band freqs: the offsets are all 0, the index array is empty and no mask value is read
+    out0 = empty((B * C, F // C, T, 2), F32)
+    out0.fill_(7.0)
+    mbrt.band_mask_merge(to_dev(stft, F32), [torch.zeros(2, device="cuda")], to_dev(np.zeros(F + 1, np.int32), I32),
+                         torch.empty(0, dtype=torch.int32, device="cuda"), to_dev(np.zeros(F, np.float32), F32), out0, C)
+    torch.cuda.synchronize()
+    assert (to_host(out0, F32) == 0).all()
+
+
 def test_zero_dc(orc, dev):
     say("zero_dc")
     for dt in (F32, BF16):
