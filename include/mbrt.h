@@ -430,7 +430,9 @@ MBRT_API int mbrt_istft(const void* spec, int spec_dtype, const float* window, f
  * with MBRT_E_SHAPE).  Every call on one GPU shares that array, so calls that overlap on
  * one GPU (concurrent streams, threads) race.  Same results as mbrt_istft, bit for bit.
  * No counterpart in the reference: it is for callers that cannot allocate device memory,
- * such as code under HIP graph capture and tight serving loops. */
+ * such as tight serving loops and code under HIP graph capture.  The first call on a GPU
+ * looks up that GPU's scratch address (hipGetSymbolAddress): make it outside any capture;
+ * later calls issue kernel launches only and can be captured and replayed. */
 MBRT_API int mbrt_istft_noalloc(const void* spec, int spec_dtype, const float* window, float* out,
                                 int64_t batch, int64_t freq_bins, int64_t frames, int64_t n_fft, int64_t hop,
                                 int64_t win_length, int64_t window_numel, int center, int normalized,

@@ -400,8 +400,9 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
 
     // CSR offsets of the tile's freqs: lane l holds off[f0 + l] (l <= nf), broadcast by readlane
     const int off_lane = ld_idx<I64>(a.off, f0 + min(lane, nf));
+    // with no band-bins (J = 0) no entry is read, whatever the offsets hold
     const int e_begin = __builtin_amdgcn_readlane(off_lane, 0);
-    const int e_end = __builtin_amdgcn_readlane(off_lane, nf);
+    const int e_end = a.J > 0 ? __builtin_amdgcn_readlane(off_lane, nf) : e_begin;
     float c = load1(a.cnt, a.cdt, f0 + min(lane, nf - 1));
     const float inv_lane = 1.0f / (c > 1.0e-8f ? c : 1.0e-8f);
 
@@ -557,8 +558,8 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
     a.mask[0] = masks[0];
     a.mask[1] = num_stems == 2 ? masks[1] : masks[0];
     a.off = csr_offsets;
-    // with no band freqs (csr_indices may then be NULL) the clamped index loads of offsets
-    // that are not all zero read the offsets instead
+    // with no band-bins csr_indices may be NULL: the kernel then reads no index and no mask
+    // (a.J = 0), and every output is 0 / max(count, 1e-8) = 0
     a.ind = n_band_freqs > 0 ? csr_indices : csr_offsets;
     a.cnt = counts;
     a.out = out;
@@ -566,7 +567,7 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
     a.S = num_stems;
     a.F = (int)total_freq;
     a.T = (int)frames;
-    a.J = (int)std::max<int64_t>(n_band_freqs, 1);
+    a.J = (int)n_band_freqs;
     a.C = make_fastdiv((uint32_t)channels);
     const int64_t tiles = ceil_div(total_freq, kTF) * ceil_div(frames, kTT) * B * num_stems;
     MBRT_REQUIRE(tiles < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many tiles", op);

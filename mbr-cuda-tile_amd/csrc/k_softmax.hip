@@ -152,6 +152,10 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
             }
         }
     }
+    // Direct-to-LDS data is only in LDS once this wave's loads have completed (vmcnt), and
+    // the workgroup-scope fence of __syncthreads() is not required to wait for them: wait
+    // explicitly, then the barrier makes every wave's part of the span visible.
+    if constexpr (kDma) wait_vmcnt<0>();
     __syncthreads();
     auto get = [&](int e) -> float {
         if constexpr (!K16) return buf[e];

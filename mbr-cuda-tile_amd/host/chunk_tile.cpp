@@ -1,12 +1,14 @@
 // chunk_tile:: on the C-ABI (mbrt_chunk_accumulate, mbrt_chunk_normalize,
-// mbrt_chunk_fade_window) and the chunked-inference driver, host code mirroring
-// src/inference_app.cpp:72-232 step for step.
+// mbrt_chunk_fade_window) and a chunked-inference driver with the semantics of the
+// reference's chunk loop (src/inference_app.cpp:72-232): a chunk plan is built first, then
+// the model runs over groups of planned chunks and their outputs are overlap-added.
 #include "chunk_tile.h"
 
 #include <algorithm>
 #include <stdexcept>
 
 #include "abi_call.h"
+#include "mbr_tile.h"
 
 namespace cudasep::chunk_tile {
 
@@ -45,96 +47,139 @@ std::vector<float> fade_window(int chunk_size, int fade_size, bool first, bool l
     return w;
 }
 
+namespace {
+
+// How the part of a model input past the signal's end is filled.
+enum class TailFill { None, Reflect, Zero };
+
+// One model input of the chunked pass, in samples of the (possibly border-padded) signal.
+struct ChunkSpan {
+    int64_t offset;   // first sample
+    int64_t taken;    // samples taken from the signal, <= chunk size
+    TailFill tail;    // fill of [taken, chunk size)
+    bool song_start;  // no fade-in: nothing overlaps this chunk's start
+    bool song_end;    // no fade-out: this chunk reaches the end of the signal
+};
+
+struct ChunkPlan {
+    int64_t source_len = 0;  // samples of the caller's signal
+    int64_t border = 0;      // reflect border added at both ends (0: none)
+    int64_t work_len = 0;    // samples of the bordered signal: the accumulator length
+    int per_call = 1;        // chunks stacked into one model call
+    std::vector<ChunkSpan> spans;
+};
+
+// Semantics of the reference's chunk loop (src/inference_app.cpp:72-232): a border of
+// chunk_size - step is reflected onto both ends when the signal is longer than two
+// borders; chunks start every `step` samples of the bordered signal; a chunk cut short by
+// the end is completed by reflection when it holds more than half a chunk, else by zeros.
+ChunkPlan plan_chunks(int64_t length, int chunk_size, int step, int chunk_batch_size) {
+    ChunkPlan plan;
+    plan.source_len = length;
+    const int64_t border = (int64_t)chunk_size - step;
+    plan.border = border > 0 && length > 2 * border ? border : 0;
+    plan.work_len = length + 2 * plan.border;
+    for (int64_t at = 0; at < plan.work_len; at += step) {
+        const int64_t taken = std::min<int64_t>(chunk_size, plan.work_len - at);
+        const TailFill tail = taken == chunk_size ? TailFill::None
+                              : 2 * taken > chunk_size ? TailFill::Reflect
+                                                       : TailFill::Zero;
+        plan.spans.push_back({at, taken, tail, at == 0, at + taken >= plan.work_len});
+    }
+    const int64_t n = (int64_t)plan.spans.size();
+    plan.per_call = (int)std::max<int64_t>(1, std::min<int64_t>(chunk_batch_size, n));
+    return plan;
+}
+
+// Sets the reference's per-thread time-attention chunk index for the duration of one model
+// call (src/inference_app.cpp:32-40), back to -1 afterwards.
+class AttentionChunkScope {
+public:
+    explicit AttentionChunkScope(int64_t index) { mbr_tile::set_time_attention_context_chunk((int)index); }
+    ~AttentionChunkScope() { mbr_tile::set_time_attention_context_chunk(-1); }
+    AttentionChunkScope(const AttentionChunkScope&) = delete;
+    AttentionChunkScope& operator=(const AttentionChunkScope&) = delete;
+};
+
+}  // namespace
+
 Tensor process_chunked(const Tensor& audio, int chunk_size, int step, int chunk_batch_size,
                        const std::function<Tensor(const Tensor&)>& model_forward,
                        const std::function<void(const std::string&)>& logger) {
     if (chunk_size <= 0 || step <= 0) throw std::runtime_error("process_chunked: chunk_size and step must be positive");
-    Tensor mix = audio;
-    const int64_t length_init = audio.size(-1);
-    const int fade_size = chunk_size / 10;
-    const int border = chunk_size - step;
-    const bool padded = length_init > 2LL * border && border > 0;
-    if (padded) mix = mix.pad_reflect({border, border});
+    const ChunkPlan plan = plan_chunks(audio.size(-1), chunk_size, step, chunk_batch_size);
+    const Tensor signal = plan.border ? audio.pad_reflect({plan.border, plan.border}) : audio;
+    const int64_t n_chunks = (int64_t)plan.spans.size();
 
-    const int64_t total_samples = mix.size(-1);
-    std::vector<int64_t> chunk_starts;
-    for (int64_t start = 0; start < total_samples; start += step) chunk_starts.push_back(start);
-    const int64_t chunk_count = (int64_t)chunk_starts.size();
-    const int effective_batch = std::max(1, (int)std::min<int64_t>((int64_t)chunk_batch_size, chunk_count));
-    const bool single_chunk_mode = effective_batch == 1;
-
-    auto prepare_input_chunk = [&](int64_t start, int64_t end) {
-        Tensor chunk = mix.slice(-1, start, end);
-        const int64_t actual_len = end - start;
-        if (actual_len < chunk_size) {
-            if (actual_len > chunk_size / 2) chunk = chunk.pad_reflect({0, chunk_size - actual_len});
-            else chunk = chunk.pad({0, chunk_size - actual_len}, 0.0f);
+    // model input of one span: [.., C, chunk_size]
+    auto input_of = [&](const ChunkSpan& c) {
+        const Tensor part = signal.slice(-1, c.offset, c.offset + c.taken);
+        const int64_t fill = chunk_size - c.taken;
+        switch (c.tail) {
+            case TailFill::Reflect: return part.pad_reflect({0, fill});
+            case TailFill::Zero: return part.pad({0, fill}, 0.0f);
+            default: return part;
         }
-        return chunk;
     };
-    auto run_group = [&](int64_t group_start, int group_size) {
-        if (single_chunk_mode) {
-            const int64_t start = chunk_starts[(size_t)group_start];
-            return model_forward(prepare_input_chunk(start, std::min<int64_t>(start + chunk_size, total_samples)));
+    // the interior fade window is shared; the song's first and last chunks get their own
+    const std::vector<float> interior = fade_window(chunk_size, chunk_size / 10, false, false);
+    const Tensor interior_w = Tensor::from_cpu_f32(interior.data(), {(int64_t)chunk_size});
+    auto window_of = [&](const ChunkSpan& c) {
+        Tensor w = interior_w;
+        if (chunk_size / 10 > 0 && (c.song_start || c.song_end)) {
+            const std::vector<float> edge = fade_window(chunk_size, chunk_size / 10, c.song_start, c.song_end);
+            w = Tensor::from_cpu_f32(edge.data(), {(int64_t)chunk_size});
         }
-        std::vector<Tensor> inputs;
-        for (int local = 0; local < group_size; ++local) {
-            const int64_t start = chunk_starts[(size_t)(group_start + local)];
-            inputs.push_back(prepare_input_chunk(start, std::min<int64_t>(start + chunk_size, total_samples)));
-        }
-        return model_forward(Tensor::cat(inputs, 0));
+        return c.taken < chunk_size ? w.slice(0, 0, c.taken).contiguous() : w;
     };
 
-    Tensor first_batch_out = run_group(0, (int)std::min<int64_t>(effective_batch, chunk_count));
-    std::vector<int64_t> out_shape = first_batch_out.shape();
-    out_shape[0] = 1;
-    out_shape.back() = total_samples;
+    if (logger)
+        logger("chunked pass: " + std::to_string(n_chunks) + " chunk(s) of " + std::to_string(chunk_size) +
+               " samples every " + std::to_string(step) + ", " + std::to_string(plan.per_call) + " per model call");
 
-    const std::vector<float> fade = fade_window(chunk_size, fade_size, false, false);
-    const Tensor fade_tensor = Tensor::from_cpu_f32(fade.data(), {(int64_t)chunk_size});
-
-    Tensor output = Tensor::zeros(out_shape);
-    Tensor weight_sum = Tensor::zeros({total_samples});
-    const int64_t num_channels = output.numel() / total_samples;
-    output = output.reshape({num_channels, total_samples});
-
-    if (logger) {
-        logger("[chunk] start");
-        logger("[chunk] size: " + std::to_string(chunk_size));
-        logger("[chunk] step: " + std::to_string(step));
-        logger("[chunk] count: " + std::to_string(chunk_count));
-        logger("[chunk] batch size: " + std::to_string(effective_batch));
-    }
-    int64_t chunk_index = 0;
-    for (int64_t group_start = 0; group_start < chunk_count; group_start += effective_batch) {
-        const int group_size = (int)std::min<int64_t>(effective_batch, chunk_count - group_start);
-        const Tensor batch_out = group_start == 0 ? first_batch_out : run_group(group_start, group_size);
-        for (int local = 0; local < group_size; ++local) {
-            const int64_t start = chunk_starts[(size_t)(group_start + local)];
-            const int64_t end = std::min<int64_t>(start + chunk_size, total_samples);
-            const int64_t actual_len = end - start;
-            const bool last_chunk = end >= total_samples;
-            ++chunk_index;
-            Tensor chunk_out = single_chunk_mode ? batch_out : batch_out.slice(0, local, local + 1).contiguous();
-            if (chunk_out.size(-1) > actual_len) chunk_out = chunk_out.slice(-1, 0, actual_len);
-            chunk_out = chunk_out.contiguous().reshape({num_channels, actual_len});
-            Tensor window = fade_tensor;
-            if (fade_size > 0 && (start == 0 || last_chunk)) {
-                const std::vector<float> w = fade_window(chunk_size, fade_size, start == 0, last_chunk);
-                window = Tensor::from_cpu_f32(w.data(), {(int64_t)chunk_size});
+    // accumulators, shaped from the first model output: [1, .., work_len] seen as [channels, work_len]
+    std::vector<int64_t> result_shape;
+    Tensor acc, weights;
+    int64_t channels = 0;
+    for (int64_t first = 0; first < n_chunks; first += plan.per_call) {
+        const int64_t count = std::min<int64_t>(plan.per_call, n_chunks - first);
+        Tensor out;
+        {
+            const AttentionChunkScope scope(first);
+            if (count == 1) {
+                out = model_forward(input_of(plan.spans[(size_t)first]));
+            } else {
+                std::vector<Tensor> inputs;
+                inputs.reserve((size_t)count);
+                for (int64_t i = 0; i < count; ++i) inputs.push_back(input_of(plan.spans[(size_t)(first + i)]));
+                out = model_forward(Tensor::cat(inputs, 0));
             }
-            const Tensor fade_crop = actual_len < chunk_size ? window.slice(0, 0, actual_len).contiguous() : window;
-            accumulate_chunk(output, weight_sum, chunk_out, fade_crop, start);
-            if (logger && (chunk_index == 1 || chunk_index == chunk_count || (chunk_index % 4) == 0))
-                logger("[chunk] completed " + std::to_string(chunk_index) + "/" + std::to_string(chunk_count));
         }
+        if (channels == 0) {
+            result_shape = out.shape();
+            result_shape.front() = 1;
+            result_shape.back() = plan.work_len;
+            int64_t per_sample = 1;
+            for (size_t d = 0; d + 1 < result_shape.size(); ++d) per_sample *= result_shape[d];
+            channels = per_sample;
+            acc = Tensor::zeros({channels, plan.work_len});
+            weights = Tensor::zeros({plan.work_len});
+        }
+        for (int64_t i = 0; i < count; ++i) {
+            const ChunkSpan& c = plan.spans[(size_t)(first + i)];
+            Tensor piece = count == 1 ? out : out.slice(0, i, i + 1).contiguous();
+            if (piece.size(-1) > c.taken) piece = piece.slice(-1, 0, c.taken);
+            accumulate_chunk(acc, weights, piece.contiguous().reshape({channels, c.taken}), window_of(c), c.offset);
+        }
+        if (logger)
+            logger("chunked pass: " + std::to_string(first + count) + " of " + std::to_string(n_chunks) +
+                   " chunk(s) merged");
     }
-    if (logger) logger("[chunk] merge complete");
 
-    normalize_by_weights(output, weight_sum);
-    output = output.reshape(out_shape);
-    if (padded) output = output.slice(output.ndim() - 1, border, border + length_init);
-    return output;
+    normalize_by_weights(acc, weights);
+    Tensor result = acc.reshape(result_shape);
+    if (plan.border) result = result.slice(result.ndim() - 1, plan.border, plan.border + plan.source_len);
+    return result;
 }
 
 }  // namespace cudasep::chunk_tile

@@ -91,6 +91,18 @@ bool residual_rms_norm_fused_path_enabled() {
     return g_quantize_bf16 && !env_flag_enabled("CUDASEP_DISABLE_RESIDUAL_RMS_NORM_FUSED");
 }
 
+// ---- time-attention context: per-thread indices, -1 when unset ---------------------------
+
+namespace {
+thread_local int t_attention_chunk = -1;
+thread_local int t_attention_depth = -1;
+}  // namespace
+
+void set_time_attention_context_chunk(int chunk_index) { t_attention_chunk = chunk_index; }
+void set_time_attention_context_depth(int depth_index) { t_attention_depth = depth_index; }
+int time_attention_context_chunk() { return t_attention_chunk; }
+int time_attention_context_depth() { return t_attention_depth; }
+
 // ---- normalisation ----------------------------------------------------------------------
 
 Tensor rms_norm(const Tensor& x, const Tensor& gamma, float scale) {

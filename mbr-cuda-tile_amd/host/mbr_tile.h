@@ -19,6 +19,16 @@ bool bands_per_freq_bf16_enabled();
 bool rotary_freqs_bf16_enabled();
 bool residual_rms_norm_fused_path_enabled();
 
+// ---- time-attention context (src/mbr_cuda_tile.h:92-94, src/mbr_cuda_tile.cu:83-84,
+// 5988-5994).  Per-thread chunk and depth indices that the application sets around each
+// model call (src/inference_app.cpp:32-40) and the model around each time-transformer
+// layer (src/model_mel_band_roformer.cu:745-802); -1 means unset.  No op depends on them,
+// as in the reference; the getters let a caller read back what it set.
+void set_time_attention_context_chunk(int chunk_index);
+void set_time_attention_context_depth(int depth_index);
+int time_attention_context_chunk();
+int time_attention_context_depth();
+
 // ---- normalisation
 // y = x * scale * gamma / sqrt(sum x^2 + 1e-12) over the last dim (src/mbr_cuda_tile.cu:6297-6373).
 // Output BF16 under the RMS-norm bf16 policy, else F32 (F16 for F16 input).

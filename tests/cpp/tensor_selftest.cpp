@@ -248,6 +248,55 @@ void unit() {
         HIP_CHECK(hipStreamDestroy(s1));
         HIP_CHECK(hipStreamDestroy(s2));
     }
+
+    // set_stream while the current stream is being captured into a graph: it must not
+    // synchronize (that would invalidate the capture); the new stream joins the capture,
+    // and switching back joins it again, so the capture ends cleanly.  The graph is then
+    // replayed several times with eager work in between, each replay checked.
+    {
+        auto& ctx = cudasep::HipContext::instance();
+        hipStream_t s1 = nullptr, s2 = nullptr;
+        HIP_CHECK(hipStreamCreate(&s1));
+        HIP_CHECK(hipStreamCreate(&s2));
+        ctx.set_stream(s1);
+        Tensor y = Tensor::empty({4096});  // allocated before the capture
+        y.fill_(0.0f);
+        ctx.synchronize();
+        HIP_CHECK(hipStreamBeginCapture(s1, hipStreamCaptureModeRelaxed));
+        bool switched = true;
+        try {
+            y.fill_(2.0f);     // captured on s1
+            ctx.set_stream(s2);
+            y.add_(y);         // captured on s2, after the fill
+            ctx.set_stream(s1);
+            y.mul_scalar_(3.0f);  // captured on s1, after the add
+        } catch (const std::exception& e) {
+            std::cout << "  message: " << e.what() << std::endl;
+            switched = false;
+            ctx.set_stream(s1);
+        }
+        hipGraph_t graph = nullptr;
+        const hipError_t end = hipStreamEndCapture(s1, &graph);
+        check(switched && end == hipSuccess && graph != nullptr, "set_stream inside a capture keeps the capture valid");
+        if (end == hipSuccess && graph != nullptr) {
+            hipGraphExec_t exec = nullptr;
+            HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+            bool all = true;
+            for (int rep = 0; rep < 3; ++rep) {
+                y.fill_(-1.0f);  // eager work between replays
+                ctx.synchronize();
+                HIP_CHECK(hipGraphLaunch(exec, s1));
+                HIP_CHECK(hipStreamSynchronize(s1));
+                all = all && same(y.to_cpu_f32(), std::vector<float>(4096, 12.0f));
+            }
+            check(all, "graph captured across set_stream replays (2 + 2) * 3 = 12, three times");
+            HIP_CHECK(hipGraphExecDestroy(exec));
+            HIP_CHECK(hipGraphDestroy(graph));
+        }
+        ctx.set_stream(nullptr);
+        HIP_CHECK(hipStreamDestroy(s1));
+        HIP_CHECK(hipStreamDestroy(s2));
+    }
 }
 
 // ---- ops mode: raw little-endian inputs/outputs named in <dir>/manifest.txt -------------
@@ -370,12 +419,27 @@ void ops(const std::string& path) {
         };
         std::vector<std::string> log;
         auto logger = [&log](const std::string& m) { log.push_back(m); };
+        // the model sees the index of the first chunk of its call as the time-attention
+        // chunk context, and the context is unset again after the pass
+        std::vector<int> seen;
+        auto identity_ctx = [&seen](const Tensor& x) {
+            seen.push_back(cudasep::mbr_tile::time_attention_context_chunk());
+            return x.clone();
+        };
         d.save("chunk_a_b1", K::process_chunked(I["audio_a"], 4000, 3000, 1, identity));
-        d.save("chunk_a_b4", K::process_chunked(I["audio_a"], 4000, 3000, 4, identity, logger));
+        d.save("chunk_a_b4", K::process_chunked(I["audio_a"], 4000, 3000, 4, identity_ctx, logger));
         d.save("chunk_b_2stem", K::process_chunked(I["audio_b"], 4000, 3200, 2, two_stems));
         d.save("chunk_c_short", K::process_chunked(I["audio_c"], 4000, 3000, 3, identity));
-        if (log.empty() || log.front() != "[chunk] start" || log.back() != "[chunk] merge complete")
+        if (log.size() != seen.size() + 1 || log.front().rfind("chunked pass: ", 0) != 0 ||
+            log.back().find(" chunk(s) merged") == std::string::npos)
             throw std::runtime_error("chunk_tile::process_chunked: unexpected log lines");
+        bool ctx_ok = !seen.empty() && cudasep::mbr_tile::time_attention_context_chunk() == -1;
+        for (size_t i = 0; i < seen.size(); ++i) ctx_ok = ctx_ok && seen[i] == 4 * (int)i;
+        if (!ctx_ok) throw std::runtime_error("chunk_tile::process_chunked: unexpected attention chunk context");
+        cudasep::mbr_tile::set_time_attention_context_depth(3);
+        if (cudasep::mbr_tile::time_attention_context_depth() != 3)
+            throw std::runtime_error("mbr_tile::set_time_attention_context_depth not kept");
+        cudasep::mbr_tile::set_time_attention_context_depth(-1);
     }
     cudasep::g_quantize_bf16 = false;
     cudasep::HipContext::instance().synchronize();

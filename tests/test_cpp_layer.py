@@ -56,6 +56,7 @@ API = [
     "cudasep::mbr_tile::rotary_freqs_bf16_enabled(", "cudasep::mbr_tile::scaled_dot_product_attention(",
     "cudasep::mbr_tile::scaled_dot_product_attention_time_split_contig(",
     "cudasep::mbr_tile::scaled_dot_product_attention_time_split_contig_q_rotary(",
+    "cudasep::mbr_tile::set_time_attention_context_chunk(", "cudasep::mbr_tile::set_time_attention_context_depth(",
     "cudasep::stft_tile::hann_window(", "cudasep::stft_tile::stft(", "cudasep::stft_tile::istft(",
     "cudasep::chunk_tile::accumulate_chunk(", "cudasep::chunk_tile::normalize_by_weights(",
     "cudasep::chunk_tile::process_chunked(",

@@ -49,3 +49,32 @@ def test_istft_noalloc_rejects_calls_beyond_the_scratch(dev):
     assert "scratch" in str(e.value)
     torch.cuda.synchronize()
     assert float(out.abs().max()) == 0.0  # nothing ran
+
+
+def test_istft_noalloc_under_graph_capture(dev):
+    # The first call on a GPU resolves the scratch array's device address (a runtime call
+    # that is not a stream operation), so it is made outside the capture.  After that a
+    # call allocates nothing and issues only kernel launches, and a captured call replays
+    # with whatever the spectrum holds at replay time.  Each replay follows eager work
+    # (new spectrum data, the workspace form into another buffer) and is checked bit for
+    # bit against it.
+    B, T, hop = 2, 64, 441
+    say(f"istft_noalloc under graph capture B={B} T={T} hop={hop}")
+    g = torch.Generator(device="cuda").manual_seed(0x4D425200C3)
+    spec = torch.randn((B, 1025, T, 2), generator=g, device="cuda")
+    win = mbrt.hann_window(2048)
+    out = torch.empty((B, mbrt.istft_output_length(T, hop, True, -1)), device="cuda")
+    mbrt.istft_noalloc(spec, win, hop, out)  # warm-up on this GPU, outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mbrt.istft_noalloc(spec, win, hop, out)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        spec.copy_(torch.randn((B, 1025, T, 2), generator=g, device="cuda"))
+        ref = mbrt.istft(spec, win, hop)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(out, F32), to_host(ref, F32), f"graph replay {rep} = istft")
