@@ -169,6 +169,15 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
     };
     const int lane = tid % G;
     const int last = a.cols - 1;
+    // Rows of 33..64 elements (8 groups of 8 lanes per wave, 64 slots per row): each wave
+    // instruction reads 8 rows, `cols` elements apart.  Group g walks its row's slots from
+    // rot = g (8 - cols) mod 64 on, slot (lane + 8 k + rot) mod 64, so that the 8 blocks of
+    // an instruction start at element 8 g + 8 k (mod 64) of the span's 32-bank window:
+    // every group reads its own 4 (2-byte) or 8 (f32) banks, with no bank conflict.  Slots
+    // at or past `cols` are masked; their reads stay inside the span's LDS buffer.
+    constexpr bool kRot = G == 8 && NM == 8;
+    const int rot = kRot ? (((tid / G) % (64 / G)) * (8 - a.cols)) & 63 : 0;
+    auto slot = [&](int k) { return kRot ? (lane + G * k + rot) & 63 : lane + G * k; };
 #pragma unroll
     for (int rr = 0; rr < RPG; ++rr) {
         const int r = tid / G + rr * (kThreads / G);
@@ -177,8 +186,9 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
         float m = -INFINITY;
 #pragma unroll
         for (int k = 0; k < NM; ++k) {
-            const float x = get(rbase + min(lane + G * k, last));
-            z[k] = lane + G * k <= last ? x * a.scale_log2e : -INFINITY;
+            const int e = slot(k);
+            const float x = get(rbase + (kRot ? e : min(e, last)));
+            z[k] = e <= last ? x * a.scale_log2e : -INFINITY;
             m = fmaxf(m, z[k]);
         }
         m = group_max<G>(m);
@@ -193,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
         if (r < nrows) {
 #pragma unroll
             for (int k = 0; k < NM; ++k)
-                if (lane + G * k <= last) put(rbase + lane + G * k, z[k] * inv);
+                if (slot(k) <= last) put(rbase + slot(k), z[k] * inv);
         }
     }
     __syncthreads();
