@@ -24,6 +24,7 @@ constexpr int kUGate = MBRT_GATE_U; // sigmoid gate x head merge
 constexpr int kNoBias = -1;  // bias dtype tag: no bias
 
 __device__ __forceinline__ int64_t clamp_group(int64_t g, int64_t groups) { return g < groups ? g : groups - 1; }
+__device__ __forceinline__ int64_t ceil_div_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // GELU rounded to bf16/f16 uses the A&S 7.1.26 complement; f32 output uses erfcf.
 template <bool LOWP>
@@ -172,7 +173,10 @@ struct GateArgs {
 template <int ADT, int GDT, int ODT>
 __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
     constexpr int VE = (ADT == F32 || ODT == F32) ? 4 : 8;
-    const int64_t base = (int64_t)blockIdx.x * (kThreads * kUGate) + threadIdx.x;
+    // chunks of kThreads * kUGate groups; a grid smaller than the chunk count walks them
+    const int64_t chunks = ceil_div_dev(a.groups, (int64_t)kThreads * kUGate);
+    for (int64_t chunk = blockIdx.x; chunk < chunks; chunk += gridDim.x) {
+    const int64_t base = chunk * (kThreads * kUGate) + threadIdx.x;
     Vec<ADT, VE> av[kUGate];
     float gl[kUGate];
 #pragma unroll
@@ -205,6 +209,7 @@ __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
             o.from_f32(v);
             o.template store<MBRT_NT_GATE>(a.out, g * VE);
         }
+    }
     }
 }
 
@@ -355,7 +360,9 @@ int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const void* gate, 
             with_dt(gate_dtype, [&](auto gt) {
                 with_dt(out_dtype, [&](auto ot) {
                     constexpr int A = decltype(at)::value, G = decltype(gt)::value, O = decltype(ot)::value;
-                    hipLaunchKernelGGL((gate_merge_vec_kernel<A, G, O>), vec_grid(a.groups, kUGate), dim3(kThreads), 0, st, a);
+                    dim3 grid = vec_grid(a.groups, kUGate);
+                    if (MBRT_GATE_BPC > 0) grid.x = (unsigned)std::min<int64_t>(grid.x, (int64_t)cu_count() * MBRT_GATE_BPC);
+                    hipLaunchKernelGGL((gate_merge_vec_kernel<A, G, O>), grid, dim3(kThreads), 0, st, a);
                 });
             });
         });

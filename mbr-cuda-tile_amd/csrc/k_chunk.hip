@@ -84,6 +84,37 @@ __global__ __launch_bounds__(kThreads) void accumulate_vec_kernel(AccArgs a) {
     }
 }
 
+// One wave per channel: a block of CPB waves takes channels [CPB y, CPB y + CPB) over the
+// same 64 consecutive float4 positions of the chunk, so the window's repeated reads are
+// made by waves of one CU, close together in time (float4 units as above).
+template <int CPB>
+__global__ __launch_bounds__(64 * CPB) void accumulate_cw_kernel(AccArgs a) {
+    const int lane = threadIdx.x % 64, w = threadIdx.x / 64;
+    const int64_t c = (int64_t)blockIdx.y * CPB + w;
+    for (int64_t k = (int64_t)blockIdx.x * 64 + lane; k < a.n; k += (int64_t)gridDim.x * 64) {
+        const float4 wv = reinterpret_cast<const float4*>(a.win)[k];
+        if (c < a.channels) {
+            const float4 s = reinterpret_cast<const float4*>(a.src)[c * a.n + k];
+            float4* dp = reinterpret_cast<float4*>(a.dest) + c * a.dest_len + a.offset + k;
+            float4 d = *dp;
+            d.x = acc1(d.x, s.x, wv.x);
+            d.y = acc1(d.y, s.y, wv.y);
+            d.z = acc1(d.z, s.z, wv.z);
+            d.w = acc1(d.w, s.w, wv.w);
+            *dp = d;
+        }
+        if (blockIdx.y == 0 && w == 0) {
+            float4* wp = reinterpret_cast<float4*>(a.wsum) + a.offset + k;
+            float4 ws = *wp;
+            ws.x = ws.x + wv.x;
+            ws.y = ws.y + wv.y;
+            ws.z = ws.z + wv.z;
+            ws.w = ws.w + wv.w;
+            *wp = ws;
+        }
+    }
+}
+
 struct NormArgs {
     float* __restrict__ data;        // [C, len]
     const float* __restrict__ wsum;  // [len]
@@ -144,7 +175,14 @@ int mbrt_chunk_accumulate(float* dest, float* weight_sum, const float* src, cons
         a.n /= 4;
         a.dest_len /= 4;
         a.offset /= 4;
-        hipLaunchKernelGGL(accumulate_vec_kernel, dim3((unsigned)grid_for(a.n), gy), dim3(kThreads), 0, st, a);
+        if (MBRT_CHUNK_CPB > 0) {
+            constexpr int CPB = MBRT_CHUNK_CPB > 0 ? MBRT_CHUNK_CPB : 1;
+            const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(a.n, 64), int64_t(1) << 16);
+            hipLaunchKernelGGL(accumulate_cw_kernel<CPB>, dim3(gx, (unsigned)ceil_div(channels, CPB)), dim3(64 * CPB), 0,
+                               st, a);
+        } else {
+            hipLaunchKernelGGL(accumulate_vec_kernel, dim3((unsigned)grid_for(a.n), gy), dim3(kThreads), 0, st, a);
+        }
     } else {
         hipLaunchKernelGGL(accumulate_scalar_kernel, dim3((unsigned)grid_for(a.n), gy), dim3(kThreads), 0, st, a);
     }

@@ -97,6 +97,12 @@
 #ifndef MBRT_GATE_U
 #define MBRT_GATE_U 2    // 16-byte groups per thread: sigmoid gate x head merge
 #endif
+#ifndef MBRT_GATE_BPC
+#define MBRT_GATE_BPC 16  // sigmoid gate x head merge: blocks per CU of a grid that walks the chunks (0: one chunk per block)
+#endif
+#ifndef MBRT_CHUNK_CPB
+#define MBRT_CHUNK_CPB 4  // chunk accumulate: channels (one wave each) per block over shared positions (0: one channel per grid row)
+#endif
 #ifndef MBRT_EW_U
 #define MBRT_EW_U 4      // 16-byte groups per thread in the elementwise kernels
 #endif
