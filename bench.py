@@ -226,7 +226,7 @@ def build_ops(torch, mbrt, bands):
     fade = torch.from_numpy(mbrt.chunk_fade_window(Nc, Nc // 10)).to(dev)
     op = Op("chunk_accumulate_8ch", Cc * Nc * 4 + Nc * 4 + 2 * Cc * Nc * 4 + 2 * Nc * 4,
             lambda: dict(s=randn((Cc, Nc)), d=randn((Cc, Lc)), w=torch.rand(Lc, device=dev) + 1.0),
-            "accumulate_vec_kernel")
+            "accumulate_cw_kernel")
     op.next = True
     op.run = lambda b: mbrt.chunk_accumulate(b["d"], b["w"], b["s"], fade, off_c)
     ops.append(op)
