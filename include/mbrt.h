@@ -118,6 +118,18 @@ MBRT_API int mbrt_version(void);
 /* Blocks until all work on `stream` has finished; reports asynchronous errors. */
 MBRT_API int mbrt_stream_sync(mbrt_stream_t stream);
 
+/* Arithmetic flags of the calling thread, read by every later call it makes (0 = default).
+ * MBRT_ARITH_BF16_INTERMEDIATES is the reference's full-bf16 experiment mode
+ * (full_bf16_arith_enabled(), src/mbr_cuda_tile.cu:190-192, which its host dispatch passes
+ * to the kernels as `full_bf16`): the ops below round their intermediates to bf16 at the
+ * points its kernels do, under the same dtype conditions (each op's comment says which).
+ * Ops and dtypes without such a path compute as by default.  The reference reads the
+ * switch from the environment; here the caller sets it, and mbr_tile:: does so from
+ * CUDASEP_FULL_BF16_ARITH_EXPERIMENTS under bf16.  Unknown bits are rejected. */
+enum mbrt_arith_flag { MBRT_ARITH_BF16_INTERMEDIATES = 1 };
+MBRT_API int mbrt_set_arith_flags(uint32_t flags);
+MBRT_API uint32_t mbrt_get_arith_flags(void);
+
 /* ---- flat element-wise (tensor_tile, src/tensor_cuda_tile.cu) -------------- */
 
 /* dst[i] = value for i < n.  Replaces tensor_tile::fill (src/tensor_cuda_tile.cu:403-420).
@@ -207,7 +219,9 @@ MBRT_API int mbrt_reduce_general(const float* src, float* dst, int64_t outer, in
 /* out[r, d] = x[r, d] * scale * gamma[d] / sqrt(sum_d x[r, d]^2 + eps), f32 math.
  * x: F32/F16/BF16; gamma: F32/BF16; out: F32/F16/BF16.  Rows are contiguous with
  * pitch `dim`.  Replaces mbr_tile::rms_norm (src/mbr_cuda_tile.cu:6297-6373;
- * kernels 4791-5090), which uses eps = 1e-12. */
+ * kernels 4791-5090), which uses eps = 1e-12.
+ * MBRT_ARITH_BF16_INTERMEDIATES, BF16 out (kernels 4815-4843): x, sum x^2, 1/sqrt and
+ * gamma are rounded to bf16 and out = bf16(((x * inv) * gamma) * scale). */
 MBRT_API int mbrt_rms_norm(const void* x, int x_dtype, const void* gamma, int gamma_dtype, void* out,
                   int out_dtype, int64_t rows, int64_t dim, float scale, float eps,
                   mbrt_stream_t stream);
@@ -216,7 +230,9 @@ MBRT_API int mbrt_rms_norm(const void* x, int x_dtype, const void* gamma, int ga
  * value); sum_out = s; normed = rms_norm(s).  residual/update share in_dtype.
  * sum_out may alias residual (in place) but not update.  Replaces
  * mbr_tile::try_residual_add_rms_norm (src/mbr_cuda_tile.cu:6375-6417; kernels
- * 4877-4965) without its D == 256 / bf16-only restriction. */
+ * 4877-4965) without its D == 256 / bf16-only restriction.
+ * MBRT_ARITH_BF16_INTERMEDIATES, BF16 normed: as mbrt_rms_norm of bf16(s); sum_out
+ * keeps sum_dtype. */
 MBRT_API int mbrt_residual_add_rms_norm(const void* residual, const void* update, int in_dtype,
                                const void* gamma, int gamma_dtype, void* sum_out,
                                int sum_dtype, void* normed, int normed_dtype, int64_t rows,
@@ -233,7 +249,9 @@ MBRT_API int mbrt_bias_act(const void* x, int x_dtype, const void* bias, int bia
                   int out_dtype, int64_t rows, int64_t cols, int act, mbrt_stream_t stream);
 
 /* out[r, d] = x[r, d] * sigmoid(x[r, half_dim + d]) for x [rows, 2 * half_dim].
- * Replaces mbr_tile::glu_last_dim (src/mbr_cuda_tile.cu:8123-8165; kernels 5880-5942). */
+ * Replaces mbr_tile::glu_last_dim (src/mbr_cuda_tile.cu:8123-8165; kernels 5880-5942).
+ * MBRT_ARITH_BF16_INTERMEDIATES, BF16 in and out (5918-5940): the sigmoid is rounded
+ * to bf16 before the product. */
 MBRT_API int mbrt_glu_last_dim(const void* x, int x_dtype, void* out, int out_dtype, int64_t rows,
                       int64_t half_dim, mbrt_stream_t stream);
 
@@ -242,7 +260,9 @@ MBRT_API int mbrt_glu_last_dim(const void* x, int x_dtype, void* out, int out_dt
  * out [B,H,N,D] (MBRT_LAYOUT_BHND, the attention output) or [B,N,H,D]
  * (MBRT_LAYOUT_BNHD); gate is [B, N, H]; merged is [B, N, H*D].  Replaces
  * linear_sigmoid's add_bias_sigmoid epilogue + mbr_tile::apply_gates_and_merge_heads
- * (src/mbr_cuda_tile.cu:7907-7949, 6243-6295; kernels 4603-4789). */
+ * (src/mbr_cuda_tile.cu:7907-7949, 6243-6295; kernels 4603-4789).
+ * MBRT_ARITH_BF16_INTERMEDIATES, BF16 attn (4718-4750): g and the product are rounded
+ * to bf16, also for an F32 output. */
 MBRT_API int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const void* gate,
                             int gate_dtype, int gate_is_logit, void* merged, int out_dtype,
                             int64_t B, int64_t H, int64_t N, int64_t D, int layout,
@@ -253,7 +273,9 @@ MBRT_API int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const voi
 /* Row softmax over `cols` with f32 accumulation: z = scale*x; p = exp(z - max z) / sum.
  * in: F32/F16/BF16; out: F32/F16/BF16; out may equal in (same dtype).  Rows are
  * contiguous with pitch `cols`.  Replaces the scale_softmax* kernels
- * (src/mbr_cuda_tile.cu:5092-5285, dispatch 6663-6697) without the 2048-column limit. */
+ * (src/mbr_cuda_tile.cu:5092-5285, dispatch 6663-6697) without the 2048-column limit.
+ * MBRT_ARITH_BF16_INTERMEDIATES, BF16 in and out (5224-5281): scale * x, the max, each
+ * exp, the sum and each quotient are rounded to bf16. */
 MBRT_API int mbrt_softmax_rows(const void* in, int in_dtype, void* out, int out_dtype, int64_t rows,
                       int64_t cols, float scale, mbrt_stream_t stream);
 
@@ -265,7 +287,8 @@ MBRT_API int mbrt_softmax_rows(const void* in, int in_dtype, void* out, int out_
  * [n_pos, D/2] of trig_dtype (F32/BF16).  layout BHND: tensor [B*H, n_pos, D];
  * BNHD: [B, n_pos, H, D].  `rows` = total rows (B*H*n_pos).  Replaces
  * mbr_tile::apply_rotary_time_split_contig_inplace (src/mbr_cuda_tile.cu:7454-7530;
- * kernels 4146-4377), generalised from its fixed [B,1301,8,64] shape. */
+ * kernels 4146-4377), generalised from its fixed [B,1301,8,64] shape.
+ * MBRT_ARITH_BF16_INTERMEDIATES, BF16 data: c and s are rounded to bf16 first. */
 MBRT_API int mbrt_rotary_inplace(void* q, void* k, int dtype, const void* cos_table,
                         const void* sin_table, int trig_dtype, int64_t rows, int64_t n_pos,
                         int64_t heads, int64_t dim_head, int layout, mbrt_stream_t stream);
@@ -273,7 +296,9 @@ MBRT_API int mbrt_rotary_inplace(void* q, void* k, int dtype, const void* cos_ta
 /* Split fused qkv [B, N, 3*H*D] into q, k, v [B, H, out_N, D] with rotary on q and
  * k; rows n >= N of a padded output (out_N > N) are zero-filled in q, k and v.
  * Replaces mbr_tile::split_qkv_heads_rotary (src/mbr_cuda_tile.cu:6058-6213;
- * kernels 3897-4068, 4379-4552). */
+ * kernels 3897-4068, 4379-4552).
+ * MBRT_ARITH_BF16_INTERMEDIATES, BF16 qkv and out (4000-4068): c and s are rounded to
+ * bf16 first. */
 MBRT_API int mbrt_split_qkv_heads_rotary(const void* qkv, int qkv_dtype, const void* cos_table,
                                 const void* sin_table, int trig_dtype, void* q, void* k,
                                 void* v, int out_dtype, int64_t B, int64_t N, int64_t H,
@@ -301,7 +326,10 @@ MBRT_API int mbrt_band_gather(const float* stft, const void* freq_indices, int i
  * [B*num_stems*channels, total_freq/channels, frames, 2] of out_dtype (F32/BF16).
  * Every output element is written exactly once (no atomics, no pre-zeroing).
  * Replaces mbr_tile::apply_mask_and_scatter (src/mbr_cuda_tile.cu:7951-8081;
- * kernels 5586-5803). */
+ * kernels 5586-5803).
+ * MBRT_ARITH_BF16_INTERMEDIATES with BF16 masks (5650-5799): a BF16 out sums the masks
+ * first, rounding each partial sum to bf16, then divides stft * sum by the count and
+ * rounds; an F32 out adds each entry's bf16-rounded stft * mask / count, in ascending e. */
 MBRT_API int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_dtype,
                          int num_stems, const void* csr_offsets, const void* csr_indices,
                          int index_dtype, const void* counts, int counts_dtype, void* out,

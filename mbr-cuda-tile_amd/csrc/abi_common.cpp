@@ -6,6 +6,9 @@
 namespace mbrt {
 
 static thread_local std::string t_error;
+static thread_local uint32_t t_arith = 0;
+
+bool bf16_intermediates() { return (t_arith & MBRT_ARITH_BF16_INTERMEDIATES) != 0; }
 
 int set_error(int status, const char* fmt, ...) {
     char buf[512];
@@ -45,7 +48,16 @@ extern "C" {
 
 const char* mbrt_last_error(void) { return mbrt::t_error.c_str(); }
 
-int mbrt_version(void) { return 1 * 10000 + 0 * 100 + 0; }
+int mbrt_version(void) { return 1 * 10000 + 1 * 100 + 0; }
+
+int mbrt_set_arith_flags(uint32_t flags) {
+    if ((flags & ~(uint32_t)MBRT_ARITH_BF16_INTERMEDIATES) != 0)
+        return mbrt::set_error(MBRT_E_INVALID_ARG, "mbrt_set_arith_flags: unknown flags 0x%x", flags);
+    mbrt::t_arith = flags;
+    return MBRT_OK;
+}
+
+uint32_t mbrt_get_arith_flags(void) { return mbrt::t_arith; }
 
 int mbrt_stream_sync(mbrt_stream_t stream) {
     hipError_t e = hipStreamSynchronize(mbrt::as_stream(stream));

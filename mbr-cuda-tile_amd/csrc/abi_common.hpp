@@ -18,6 +18,9 @@ namespace mbrt {
 int set_error(int status, const char* fmt, ...);
 void clear_error();
 
+// MBRT_ARITH_BF16_INTERMEDIATES is set on the calling thread.
+bool bf16_intermediates();
+
 inline hipStream_t as_stream(mbrt_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool is_float_dt(int dt) { return dt == F32 || dt == F16 || dt == BF16; }

@@ -55,6 +55,10 @@ __device__ __forceinline__ float round_through(float v, int dt) {
     return v;
 }
 
+// Round to the nearest bf16 (ties to even) and widen back: an intermediate of the
+// bf16-intermediates mode.
+__device__ __forceinline__ float bf16r(float v) { return bf16_lo(f32_to_bf16_bits(v)); }
+
 // ---- element loads/stores with a run-time dtype (uniform across the grid) ----
 
 __device__ __forceinline__ float load1(const void* p, int dt, int64_t i) {

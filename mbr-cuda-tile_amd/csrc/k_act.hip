@@ -10,6 +10,9 @@
 // writes the merged [B, N, H*D] rows contiguously: one pass instead of the reference's
 // sigmoid epilogue pass plus a separate merge pass (src/mbr_cuda_tile.cu:5504-5534 +
 // 4752-4789).  Unaligned operands take runtime-dtype element kernels.
+// With MBRT_ARITH_BF16_INTERMEDIATES set, GLU (bf16 -> bf16) rounds the gate sigmoid to bf16
+// and the gate merge (bf16 attention) rounds the gate and the product to bf16, as the
+// reference's kernels do in full-bf16 mode (src/mbr_cuda_tile.cu:5918-5940, 4718-4750).
 #include "abi_common.hpp"
 
 #include <algorithm>
@@ -113,9 +116,10 @@ struct GluArgs {
     int64_t rows, half;
     int64_t groups;   // rows * half / VE
     FastDiv gpr;      // groups per row = half / VE
+    int fb;           // bf16 intermediates (element kernel; the vector kernel takes FB)
 };
 
-template <int XDT, int ODT>
+template <int XDT, int ODT, bool FB>
 __global__ __launch_bounds__(kThreads) void glu_vec_kernel(GluArgs a) {
     constexpr int VE = (XDT == F32 || ODT == F32) ? 4 : 8;
     const int64_t base = (int64_t)blockIdx.x * (kThreads * kUGlu) + threadIdx.x;
@@ -136,7 +140,7 @@ __global__ __launch_bounds__(kThreads) void glu_vec_kernel(GluArgs a) {
             xv[u].to_f32(v);
             gv[u].to_f32(gt);
 #pragma unroll
-            for (int i = 0; i < VE; ++i) v[i] = v[i] * sigmoidf(gt[i]);
+            for (int i = 0; i < VE; ++i) v[i] = v[i] * (FB ? bf16r(sigmoidf(gt[i])) : sigmoidf(gt[i]));
             Vec<ODT, VE> o;
             o.from_f32(v);
             o.template store<MBRT_NT_GLU>(a.out, g * VE);
@@ -150,7 +154,8 @@ __global__ __launch_bounds__(kThreads) void glu_elem_kernel(GluArgs a) {
     for (; i < n; i += (int64_t)gridDim.x * kThreads) {
         const int64_t row = i / a.half, d = i - row * a.half;
         const int64_t in0 = row * 2 * a.half + d;
-        store1(a.out, a.odt, i, load1(a.x, a.xdt, in0) * sigmoidf(load1(a.x, a.xdt, in0 + a.half)));
+        const float g = sigmoidf(load1(a.x, a.xdt, in0 + a.half));
+        store1(a.out, a.odt, i, load1(a.x, a.xdt, in0) * (a.fb ? bf16r(g) : g));
     }
 }
 
@@ -168,9 +173,10 @@ struct GateArgs {
     FastDiv gpt;       // groups per token = H*D/VE
     FastDiv gph;       // groups per head = D/VE
     FastDiv n_div;     // N
+    int fb;            // bf16 intermediates (element kernel; the vector kernel takes FB)
 };
 
-template <int ADT, int GDT, int ODT>
+template <int ADT, int GDT, int ODT, bool FB>
 __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
     constexpr int VE = (ADT == F32 || ODT == F32) ? 4 : 8;
     // chunks of kThreads * kUGate groups; a grid smaller than the chunk count walks them
@@ -202,9 +208,10 @@ __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
         if (g < a.groups) {
             float v[VE];
             av[u].to_f32(v);
-            const float gv = a.logit ? sigmoidf(gl[u]) : gl[u];
+            float gv = a.logit ? sigmoidf(gl[u]) : gl[u];
+            if constexpr (FB) gv = bf16r(gv);
 #pragma unroll
-            for (int i = 0; i < VE; ++i) v[i] *= gv;
+            for (int i = 0; i < VE; ++i) v[i] = FB ? bf16r(v[i] * gv) : v[i] * gv;
             Vec<ODT, VE> o;
             o.from_f32(v);
             o.template store<MBRT_NT_GATE>(a.out, g * VE);
@@ -227,8 +234,10 @@ __global__ __launch_bounds__(kThreads) void gate_merge_elem_kernel(GateArgs a) {
         } else {
             src = i;
         }
-        const float g = load1(a.gate, a.gdt, token * a.H + h);
-        store1(a.out, a.odt, i, load1(a.attn, a.adt, src) * (a.logit ? sigmoidf(g) : g));
+        const float gl = load1(a.gate, a.gdt, token * a.H + h);
+        const float g = a.logit ? sigmoidf(gl) : gl;
+        const float y = a.fb ? bf16r(load1(a.attn, a.adt, src) * bf16r(g)) : load1(a.attn, a.adt, src) * g;
+        store1(a.out, a.odt, i, y);
     }
 }
 
@@ -304,6 +313,7 @@ int mbrt_glu_last_dim(const void* x, int x_dtype, void* out, int out_dtype, int6
     a.odt = out_dtype;
     a.rows = rows;
     a.half = half_dim;
+    a.fb = bf16_intermediates() && x_dtype == BF16 && out_dtype == BF16;
     hipStream_t st = as_stream(stream);
     const int ve = (x_dtype == F32 || out_dtype == F32) ? 4 : 8;
     const bool vec = half_dim % ve == 0 && aligned(x, 16) && aligned(out, 16) && rows * half_dim / ve < (1ll << 32);
@@ -313,7 +323,13 @@ int mbrt_glu_last_dim(const void* x, int x_dtype, void* out, int out_dtype, int6
         with_dt(x_dtype, [&](auto xt) {
             with_dt(out_dtype, [&](auto ot) {
                 constexpr int X = decltype(xt)::value, O = decltype(ot)::value;
-                hipLaunchKernelGGL((glu_vec_kernel<X, O>), vec_grid(a.groups, kUGlu), dim3(kThreads), 0, st, a);
+                if constexpr (X == BF16 && O == BF16) {
+                    if (a.fb) {
+                        hipLaunchKernelGGL((glu_vec_kernel<X, O, true>), vec_grid(a.groups, kUGlu), dim3(kThreads), 0, st, a);
+                        return;
+                    }
+                }
+                hipLaunchKernelGGL((glu_vec_kernel<X, O, false>), vec_grid(a.groups, kUGlu), dim3(kThreads), 0, st, a);
             });
         });
     } else {
@@ -347,6 +363,8 @@ int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const void* gate, 
     a.H = H;
     a.N = N;
     a.D = D;
+    // bf16 intermediates: the reference's gate merge kernels take the flag for bf16 attention
+    a.fb = bf16_intermediates() && attn_dtype == BF16;
     hipStream_t st = as_stream(stream);
     const int ve = (attn_dtype == F32 || out_dtype == F32) ? 4 : 8;
     const bool vec = D % ve == 0 && aligned(attn, 16) && aligned(merged, 16) && total / ve < (1ll << 32) &&
@@ -362,7 +380,13 @@ int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const void* gate, 
                     constexpr int A = decltype(at)::value, G = decltype(gt)::value, O = decltype(ot)::value;
                     dim3 grid = vec_grid(a.groups, kUGate);
                     if (MBRT_GATE_BPC > 0) grid.x = (unsigned)std::min<int64_t>(grid.x, (int64_t)cu_count() * MBRT_GATE_BPC);
-                    hipLaunchKernelGGL((gate_merge_vec_kernel<A, G, O>), grid, dim3(kThreads), 0, st, a);
+                    if constexpr (A == BF16) {
+                        if (a.fb) {
+                            hipLaunchKernelGGL((gate_merge_vec_kernel<A, G, O, true>), grid, dim3(kThreads), 0, st, a);
+                            return;
+                        }
+                    }
+                    hipLaunchKernelGGL((gate_merge_vec_kernel<A, G, O, false>), grid, dim3(kThreads), 0, st, a);
                 });
             });
         });

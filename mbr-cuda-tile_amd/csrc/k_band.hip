@@ -367,7 +367,11 @@ struct MergeArgs {
 // entries of the tile's freqs are staged 64 at a time: lane e loads mask[b, t, ind[c0+e]]
 // for 16 frames, the tile is transposed through LDS, and each thread sums its freqs'
 // entries in ascending order.  All loads use clamped indices and are unconditional.
-template <int MDT, int ODT, bool I64>
+// FB (bf16 masks, bf16-intermediates mode; src/mbr_cuda_tile.cu:5650-5797): a BF16 output
+// sums the freq's masks with a bf16 rounding after every add, then divides
+// stft * sum by the count and rounds; an F32 output adds, in ascending entry order, each
+// entry's stft * mask / count rounded to bf16.
+template <int MDT, int ODT, bool I64, bool FB>
 __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     __shared__ f32x2 ms[kME][kTT + 1];
     // one linear grid; neighbouring freq tiles (whose CSR runs split cache lines of the
@@ -404,7 +408,14 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     const int e_begin = __builtin_amdgcn_readlane(off_lane, 0);
     const int e_end = a.J > 0 ? __builtin_amdgcn_readlane(off_lane, nf) : e_begin;
     float c = load1(a.cnt, a.cdt, f0 + min(lane, nf - 1));
-    const float inv_lane = 1.0f / (c > 1.0e-8f ? c : 1.0e-8f);
+    const float den_lane = c > 1.0e-8f ? c : 1.0e-8f;
+    const float inv_lane = 1.0f / den_lane;
+    // readlane reads lanes regardless of EXEC: broadcast while all lanes are active
+    float den[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; ++r)
+        den[r] = FB ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, den_lane), w + 4 * r))
+                    : 1.0f;
 
     const f32x2* srow = reinterpret_cast<const f32x2*>(a.stft) + ((int64_t)b * a.F + f0) * a.T + tq;
     f32x2 sv[kPer], acc[kPer];
@@ -433,8 +444,16 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
             const int hi = fl < nf ? min(__builtin_amdgcn_readlane(off_lane, fl + 1), c1) : lo;
             for (int e = lo; e < hi; ++e) {
                 const f32x2 m = ms[e - c0][lane];
-                acc[r].x += sv[r].x * m.x - sv[r].y * m.y;
-                acc[r].y += sv[r].x * m.y + sv[r].y * m.x;
+                if constexpr (!FB) {
+                    acc[r].x += sv[r].x * m.x - sv[r].y * m.y;
+                    acc[r].y += sv[r].x * m.y + sv[r].y * m.x;
+                } else if constexpr (ODT == BF16) {
+                    acc[r].x = bf16r(acc[r].x + m.x);
+                    acc[r].y = bf16r(acc[r].y + m.y);
+                } else {
+                    acc[r].x += bf16r((sv[r].x * m.x - sv[r].y * m.y) / den[r]);
+                    acc[r].y += bf16r((sv[r].x * m.y + sv[r].y * m.x) / den[r]);
+                }
             }
         }
         __syncthreads();
@@ -453,7 +472,14 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
             uint32_t bin, ch;
             fdivmod((uint32_t)(f0 + fl), a.C, bin, ch);
             const int64_t o = (((int64_t)bs * a.C.d + ch) * bins + bin) * a.T + t;
-            store_complex<ODT>(a.out, o, f32x2{acc[r].x * inv[r], acc[r].y * inv[r]});
+            if constexpr (!FB) {
+                store_complex<ODT>(a.out, o, f32x2{acc[r].x * inv[r], acc[r].y * inv[r]});
+            } else if constexpr (ODT == BF16) {  // rounded on the store
+                const f32x2 s = sv[r], m = acc[r];
+                store_complex<ODT>(a.out, o, f32x2{(s.x * m.x - s.y * m.y) / den[r], (s.x * m.y + s.y * m.x) / den[r]});
+            } else {
+                store_complex<ODT>(a.out, o, acc[r]);
+            }
         }
     }
 }
@@ -575,13 +601,24 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
     a.tiles_t = (uint32_t)ceil_div(frames, kTT);
     a.tiles = (uint32_t)tiles;
     const dim3 grid(a.tiles);
+    // bf16 intermediates: bf16 masks into a BF16 or F32 output, as in the reference
+    const bool fb = bf16_intermediates() && mask_dtype == BF16 && (out_dtype == BF16 || out_dtype == F32);
     with_dt(mask_dtype, [&](auto mt) {
         with_dt(out_dtype, [&](auto ot) {
             constexpr int M = decltype(mt)::value, O = decltype(ot)::value;
+            if constexpr (M == BF16 && O != F16) {
+                if (fb) {
+                    if (index_dtype == I64)
+                        hipLaunchKernelGGL((band_merge_kernel<M, O, true, true>), grid, dim3(kThreads), 0, as_stream(stream), a);
+                    else
+                        hipLaunchKernelGGL((band_merge_kernel<M, O, false, true>), grid, dim3(kThreads), 0, as_stream(stream), a);
+                    return;
+                }
+            }
             if (index_dtype == I64)
-                hipLaunchKernelGGL((band_merge_kernel<M, O, true>), grid, dim3(kThreads), 0, as_stream(stream), a);
+                hipLaunchKernelGGL((band_merge_kernel<M, O, true, false>), grid, dim3(kThreads), 0, as_stream(stream), a);
             else
-                hipLaunchKernelGGL((band_merge_kernel<M, O, false>), grid, dim3(kThreads), 0, as_stream(stream), a);
+                hipLaunchKernelGGL((band_merge_kernel<M, O, false, false>), grid, dim3(kThreads), 0, as_stream(stream), a);
         });
     });
     return check_launch(op);

@@ -14,6 +14,8 @@
 //   D = 384 bf16: 48 chunks -> G = 16 lanes x 3 chunks
 // Fallback (unaligned pointers, D not a whole number of chunks, D > 4096): one wave per
 // row with a scalar two-pass loop.
+// With MBRT_ARITH_BF16_INTERMEDIATES set and a BF16 output, both paths round their
+// intermediates to bf16 as the reference's bf16-output kernels do in full-bf16 mode.
 #include "abi_common.hpp"
 
 #include <algorithm>
@@ -36,12 +38,16 @@ struct RmsArgs {
     int nchunk;  // dim / VE
     float scale;
     float eps;
+    int fb;      // bf16 intermediates (loop kernel; the fast kernel takes it as FB)
 };
 
 // One block = 256 / G rows.  gamma * scale is staged once per block in LDS as f32.  The
 // row loads are unconditional (row and chunk indices clamped into the tensor), so all of a
 // lane's x (and residual) chunks are in flight together; stores are predicated.
-template <int XDT, int ODT, bool RES, int G, int NC>
+// FB: bf16 intermediates (src/mbr_cuda_tile.cu:4815-4843, 4870-4905): the row values (the
+// residual sum where there is one), the sum of squares, 1/sqrt and gamma are each rounded
+// to bf16, and the output is ((v * inv) * gamma) * scale.
+template <int XDT, int ODT, bool RES, int G, int NC, bool FB>
 __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
     constexpr int VE = (XDT == F32 || ODT == F32) ? 4 : 8;
     extern __shared__ float gs[];
@@ -57,7 +63,8 @@ __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
         xv[k].template load<MBRT_NT_RMS>(a.x, base + c * VE);
         if (RES) rv[k].template load<MBRT_NT_RMS>(a.res, base + c * VE);
     }
-    for (int d = threadIdx.x; d < a.dim; d += kThreads) gs[d] = load1(a.gamma, a.gdt, d) * a.scale;
+    for (int d = threadIdx.x; d < a.dim; d += kThreads)
+        gs[d] = FB ? bf16r(load1(a.gamma, a.gdt, d)) : load1(a.gamma, a.gdt, d) * a.scale;
     float v[NC][VE];
     float ss = 0.0f;
 #pragma unroll
@@ -76,7 +83,10 @@ __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
         }
         const bool in = lane + G * k <= lastc;
 #pragma unroll
-        for (int i = 0; i < VE; ++i) ss = fmaf(v[k][i], in ? v[k][i] : 0.0f, ss);
+        for (int i = 0; i < VE; ++i) {
+            const float u = FB ? bf16r(v[k][i]) : v[k][i];
+            ss = fmaf(u, in ? u : 0.0f, ss);
+        }
     }
     const int full = a.nchunk / G;
     if (RES && a.sum_out != nullptr && valid) {
@@ -90,7 +100,7 @@ __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
         }
     }
     ss = group_sum<G>(ss);
-    const float inv = rsqrtf(ss + a.eps);
+    const float inv = FB ? bf16r(rsqrtf(bf16r(ss) + a.eps)) : rsqrtf(ss + a.eps);
     __syncthreads();
     if (!valid) return;
 #pragma unroll
@@ -98,7 +108,10 @@ __global__ __launch_bounds__(kThreads) void rms_fast_kernel(RmsArgs a) {
         if (k < full || lane + G * k <= lastc) {
             const int c = lane + G * k;
 #pragma unroll
-            for (int i = 0; i < VE; ++i) v[k][i] = v[k][i] * inv * gs[c * VE + i];
+            for (int i = 0; i < VE; ++i) {
+                if constexpr (FB) v[k][i] = bf16r(bf16r(v[k][i]) * inv * gs[c * VE + i] * a.scale);
+                else v[k][i] = v[k][i] * inv * gs[c * VE + i];
+            }
             Vec<ODT, VE> o;
             o.from_f32(v[k]);
             o.template store<MBRT_NT_RMS>(a.out, base + c * VE);
@@ -119,10 +132,11 @@ __global__ __launch_bounds__(kThreads) void rms_loop_kernel(RmsArgs a) {
             v = round_through(v + load1(a.res, a.xdt, base + d), a.sdt);
             if (a.sum_out != nullptr) store1(a.sum_out, a.sdt, base + d, v);
         }
+        if (a.fb) v = bf16r(v);
         ss = fmaf(v, v, ss);
     }
     ss = group_sum<64>(ss);
-    const float inv = rsqrtf(ss + a.eps) * a.scale;
+    const float inv = a.fb ? bf16r(rsqrtf(bf16r(ss) + a.eps)) : rsqrtf(ss + a.eps) * a.scale;
     for (int d = lane; d < a.dim; d += 64) {
         float v;
         if (a.res == nullptr) {
@@ -133,33 +147,35 @@ __global__ __launch_bounds__(kThreads) void rms_loop_kernel(RmsArgs a) {
         } else {
             v = round_through(load1(a.x, a.xdt, base + d) + load1(a.res, a.xdt, base + d), a.sdt);
         }
-        store1(a.out, a.odt, base + d, v * inv * load1(a.gamma, a.gdt, d));
+        if (a.fb) store1(a.out, a.odt, base + d, bf16r(bf16r(v) * inv * bf16r(load1(a.gamma, a.gdt, d)) * a.scale));
+        else store1(a.out, a.odt, base + d, v * inv * load1(a.gamma, a.gdt, d));
     }
 }
 
-template <int XDT, int ODT, bool RES, int G, int NC>
+template <int XDT, int ODT, bool RES, int G, int NC, bool FB>
 void launch_fast(const RmsArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((rms_fast_kernel<XDT, ODT, RES, G, NC>), dim3((unsigned)ceil_div(a.rows, kThreads / G)),
+    hipLaunchKernelGGL((rms_fast_kernel<XDT, ODT, RES, G, NC, FB>), dim3((unsigned)ceil_div(a.rows, kThreads / G)),
                        dim3(kThreads), a.dim * sizeof(float), st, a);
 }
 
 // Group width / chunks per lane for `nchunk` chunks; false when the row is too long.
-template <int XDT, int ODT, bool RES>
+template <int XDT, int ODT, bool RES, bool FB>
 bool launch_chunks(const RmsArgs& a, hipStream_t st) {
     constexpr int G = MBRT_RMS_G;
     const int n = a.nchunk;
-    if (n <= 2 * G) launch_fast<XDT, ODT, RES, G, 2>(a, st);
-    else if (n <= 4 * G) launch_fast<XDT, ODT, RES, G, 4>(a, st);
-    else if (n <= 6 * G) launch_fast<XDT, ODT, RES, G, 6>(a, st);
-    else if (n <= 128) launch_fast<XDT, ODT, RES, G, 128 / G>(a, st);
-    else if (n <= 512) launch_fast<XDT, ODT, RES, 64, 8>(a, st);
-    else if (n <= 1024) launch_fast<XDT, ODT, RES, 64, 16>(a, st);
+    if (n <= 2 * G) launch_fast<XDT, ODT, RES, G, 2, FB>(a, st);
+    else if (n <= 4 * G) launch_fast<XDT, ODT, RES, G, 4, FB>(a, st);
+    else if (n <= 6 * G) launch_fast<XDT, ODT, RES, G, 6, FB>(a, st);
+    else if (n <= 128) launch_fast<XDT, ODT, RES, G, 128 / G, FB>(a, st);
+    else if (n <= 512) launch_fast<XDT, ODT, RES, 64, 8, FB>(a, st);
+    else if (n <= 1024) launch_fast<XDT, ODT, RES, 64, 16, FB>(a, st);
     else return false;
     return true;
 }
 
 int launch_rms(RmsArgs a, hipStream_t st, const char* op) {
     if (a.rows == 0) return MBRT_OK;
+    a.fb = bf16_intermediates() && a.odt == BF16;
     const int ve = (a.xdt == F32 || a.odt == F32) ? 4 : 8;
     const bool res = a.res != nullptr;
     const bool al = aligned(a.x, 16) && aligned(a.out, 16) && (!res || aligned(a.res, 16)) &&
@@ -172,7 +188,13 @@ int launch_rms(RmsArgs a, hipStream_t st, const char* op) {
         with_dt(a.xdt, [&](auto xt) {
             with_dt(a.odt, [&](auto ot) {
                 constexpr int X = decltype(xt)::value, O = decltype(ot)::value;
-                done = res ? launch_chunks<X, O, true>(a, st) : launch_chunks<X, O, false>(a, st);
+                if constexpr (O == BF16) {
+                    if (a.fb) {
+                        done = res ? launch_chunks<X, O, true, true>(a, st) : launch_chunks<X, O, false, true>(a, st);
+                        return;
+                    }
+                }
+                done = res ? launch_chunks<X, O, true, false>(a, st) : launch_chunks<X, O, false, false>(a, st);
             });
         });
     }

@@ -7,6 +7,10 @@
 // values read from the [n_pos, D/2] tables, which stay L2-resident (801 x 32 x 4 B = 100 KB each)
 // while being broadcast over batch*heads.  The position of a row is row % n_pos for
 // [B*H, N, D] and (row / H) % n_pos for [B, N, H, D].
+// With MBRT_ARITH_BF16_INTERMEDIATES set and bf16 data, cos and sin are rounded to bf16
+// before the rotation, as the reference's bf16 rotary kernels do in full-bf16 mode
+// (src/mbr_cuda_tile.cu:4033-4060 and their in-place variants); with bf16 operands the
+// products are exact in f32 and the rotated pair is rounded once, on its store.
 #include "abi_common.hpp"
 
 #include <algorithm>
@@ -29,11 +33,12 @@ struct RotArgs {
     FastDiv gpr;       // groups per row (D / VE)
     FastDiv npos_div;
     FastDiv heads_div;
+    int fb;  // bf16 intermediates (scalar kernel; the vector kernel takes FB)
 };
 
 // One thread = one VE-element group (VE/2 pairs) of q and the same group of k.  All four
 // loads (q, k, cos, sin) are issued before the rotation.
-template <int DT, int TDT, bool HAS_K>
+template <int DT, int TDT, bool HAS_K, bool FB>
 __global__ __launch_bounds__(kThreads) void rotary_vec_kernel(RotArgs a) {
     constexpr int VE = ve_for<DT>();
     const uint32_t g = blockIdx.x * kThreads + threadIdx.x;
@@ -54,6 +59,13 @@ __global__ __launch_bounds__(kThreads) void rotary_vec_kernel(RotArgs a) {
     float cs[VE / 2], sn[VE / 2], x[VE];
     cv.to_f32(cs);
     sv.to_f32(sn);
+    if constexpr (FB) {
+#pragma unroll
+        for (int i = 0; i < VE / 2; ++i) {
+            cs[i] = bf16r(cs[i]);
+            sn[i] = bf16r(sn[i]);
+        }
+    }
     q.to_f32(x);
     rotate<VE>(x, cs, sn);
     q.from_f32(x);
@@ -74,7 +86,11 @@ __global__ __launch_bounds__(kThreads) void rotary_scalar_kernel(RotArgs a) {
         const int64_t row = i / half, p = i - row * half;
         int64_t pos_row = a.layout == MBRT_LAYOUT_BNHD ? row / a.heads : row;
         const int64_t n = pos_row % a.n_pos;
-        const float c = load1(a.cosp, a.tdt, n * half + p), s = load1(a.sinp, a.tdt, n * half + p);
+        float c = load1(a.cosp, a.tdt, n * half + p), s = load1(a.sinp, a.tdt, n * half + p);
+        if (a.fb) {
+            c = bf16r(c);
+            s = bf16r(s);
+        }
         const int64_t e = row * a.D + 2 * p;
         for (int t = 0; t < 2; ++t) {
             void* buf = t == 0 ? a.q : a.k;
@@ -99,11 +115,12 @@ struct SplitArgs {
     const void* cosp;
     const void* sinp;
     int64_t B, N, H, D, outN;
+    int fb;  // bf16 intermediates (scalar kernel; the vector kernel takes FB)
 };
 
 // One thread per VE-element group of the [B, H, outN, D] outputs (q, k and v together);
 // the three qkv loads and the table loads are issued before any use.
-template <int IDT, int ODT, int TDT>
+template <int IDT, int ODT, int TDT, bool FB>
 __global__ __launch_bounds__(kThreads) void split_qkv_vec_kernel(SplitArgs a, uint32_t groups, FastDiv gpr,
                                                           FastDiv outn_div, FastDiv h_div) {
     constexpr int VE = (IDT == F32 || ODT == F32) ? 4 : 8;
@@ -131,6 +148,13 @@ __global__ __launch_bounds__(kThreads) void split_qkv_vec_kernel(SplitArgs a, ui
     vv.to_f32(xv);
     cv.to_f32(cs);
     sv.to_f32(sn);
+    if constexpr (FB) {
+#pragma unroll
+        for (int i = 0; i < VE / 2; ++i) {
+            cs[i] = bf16r(cs[i]);
+            sn[i] = bf16r(sn[i]);
+        }
+    }
     rotate<VE>(xq, cs, sn);
     rotate<VE>(xk, cs, sn);
     if (pad) {
@@ -157,7 +181,11 @@ __global__ __launch_bounds__(kThreads) void split_qkv_scalar_kernel(SplitArgs a)
         const int64_t e = orow * a.D + 2 * p;
         if (n < a.N) {
             const int64_t src = (b * a.N + n) * (3 * a.H * a.D) + h * a.D + 2 * p;
-            const float c = load1(a.cosp, a.tdt, n * half + p), s = load1(a.sinp, a.tdt, n * half + p);
+            float c = load1(a.cosp, a.tdt, n * half + p), s = load1(a.sinp, a.tdt, n * half + p);
+            if (a.fb) {
+                c = bf16r(c);
+                s = bf16r(s);
+            }
             for (int part = 0; part < 3; ++part) {
                 void* dst = part == 0 ? a.q : part == 1 ? a.k : a.v;
                 const float x0 = load1(a.qkv, a.idt, src + part * a.H * a.D);
@@ -213,6 +241,8 @@ int mbrt_rotary_inplace(void* q, void* k, int dtype, const void* cos_table, cons
     a.heads = heads;
     a.D = (int)dim_head;
     a.layout = layout;
+    // bf16 intermediates: bf16 data; the rounding only changes f32 tables
+    a.fb = bf16_intermediates() && dtype == BF16;
     hipStream_t st = as_stream(stream);
     const int ve = dtype == F32 ? 4 : 8;
     const int64_t groups = rows * dim_head / ve;
@@ -230,12 +260,19 @@ int mbrt_rotary_inplace(void* q, void* k, int dtype, const void* cos_table, cons
         const dim3 grid((unsigned)ceil_div(groups, kThreads));
         with_dt(dtype, [&](auto dt_) {
             constexpr int DTv = decltype(dt_)::value;
+            if constexpr (DTv == BF16) {
+                if (a.fb && trig_dtype == F32) {
+                    if (k != nullptr) hipLaunchKernelGGL((rotary_vec_kernel<DTv, F32, true, true>), grid, dim3(kThreads), 0, st, a);
+                    else hipLaunchKernelGGL((rotary_vec_kernel<DTv, F32, false, true>), grid, dim3(kThreads), 0, st, a);
+                    return;
+                }
+            }
             if (k != nullptr) {
-                if (trig_dtype == F32) hipLaunchKernelGGL((rotary_vec_kernel<DTv, F32, true>), grid, dim3(kThreads), 0, st, a);
-                else hipLaunchKernelGGL((rotary_vec_kernel<DTv, BF16, true>), grid, dim3(kThreads), 0, st, a);
+                if (trig_dtype == F32) hipLaunchKernelGGL((rotary_vec_kernel<DTv, F32, true, false>), grid, dim3(kThreads), 0, st, a);
+                else hipLaunchKernelGGL((rotary_vec_kernel<DTv, BF16, true, false>), grid, dim3(kThreads), 0, st, a);
             } else {
-                if (trig_dtype == F32) hipLaunchKernelGGL((rotary_vec_kernel<DTv, F32, false>), grid, dim3(kThreads), 0, st, a);
-                else hipLaunchKernelGGL((rotary_vec_kernel<DTv, BF16, false>), grid, dim3(kThreads), 0, st, a);
+                if (trig_dtype == F32) hipLaunchKernelGGL((rotary_vec_kernel<DTv, F32, false, false>), grid, dim3(kThreads), 0, st, a);
+                else hipLaunchKernelGGL((rotary_vec_kernel<DTv, BF16, false, false>), grid, dim3(kThreads), 0, st, a);
             }
         });
     } else {
@@ -274,6 +311,8 @@ int mbrt_split_qkv_heads_rotary(const void* qkv, int qkv_dtype, const void* cos_
     a.H = H;
     a.D = D;
     a.outN = out_N;
+    // bf16 intermediates: bf16 qkv to bf16 heads; the rounding only changes f32 tables
+    a.fb = bf16_intermediates() && qkv_dtype == BF16 && out_dtype == BF16;
     hipStream_t st = as_stream(stream);
     const int ve = (qkv_dtype == F32 || out_dtype == F32) ? 4 : 8;
     const int64_t groups = total / ve;
@@ -288,11 +327,18 @@ int mbrt_split_qkv_heads_rotary(const void* qkv, int qkv_dtype, const void* cos_
         with_dt(qkv_dtype, [&](auto it) {
             with_dt(out_dtype, [&](auto ot) {
                 constexpr int IDTv = decltype(it)::value, ODTv = decltype(ot)::value;
+                if constexpr (IDTv == BF16 && ODTv == BF16) {
+                    if (a.fb && trig_dtype == F32) {
+                        hipLaunchKernelGGL((split_qkv_vec_kernel<IDTv, ODTv, F32, true>), grid, dim3(kThreads), 0, st,
+                                           a, (uint32_t)groups, gpr, od, hd);
+                        return;
+                    }
+                }
                 if (trig_dtype == F32)
-                    hipLaunchKernelGGL((split_qkv_vec_kernel<IDTv, ODTv, F32>), grid, dim3(kThreads), 0, st, a,
+                    hipLaunchKernelGGL((split_qkv_vec_kernel<IDTv, ODTv, F32, false>), grid, dim3(kThreads), 0, st, a,
                                        (uint32_t)groups, gpr, od, hd);
                 else
-                    hipLaunchKernelGGL((split_qkv_vec_kernel<IDTv, ODTv, BF16>), grid, dim3(kThreads), 0, st, a,
+                    hipLaunchKernelGGL((split_qkv_vec_kernel<IDTv, ODTv, BF16, false>), grid, dim3(kThreads), 0, st, a,
                                        (uint32_t)groups, gpr, od, hd);
             });
         });

@@ -34,12 +34,19 @@ struct SmArgs {
     int64_t rows;
     int cols;
     float scale_log2e;
+    float scale;  // bf16-intermediates mode: the scale is applied (and rounded) on its own
 };
+
+// Bf16-intermediates mode (scale_softmax_bf16_to_bf16_kernel in full-bf16 mode,
+// src/mbr_cuda_tile.cu:5224-5252): z = bf16(x * scale), the row max, e = bf16(exp(z - max)),
+// the sum bf16(sum e) and p = bf16(e / sum) are each rounded to bf16.  The FB kernels are
+// instantiated for bf16 -> bf16 rows only.
+__device__ __forceinline__ float fb_exp(float z, float m) { return bf16r(__builtin_amdgcn_exp2f((z - m) * kLog2e)); }
 
 // Loads are unconditional (the row index and the element index are clamped into the
 // tensor), so all NM loads of a lane are issued before the first use; only stores are
 // predicated, and only the last slot of a row ever needs a per-lane predicate.
-template <int IDT, int G, int NM>
+template <int IDT, int G, int NM, bool FB>
 __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
     const int lane = threadIdx.x % G;
     const int64_t row = (int64_t)blockIdx.x * (kThreads / G) + threadIdx.x / G;
@@ -52,25 +59,27 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < NM; ++k) {
-        z[k] = lane + G * k <= last ? z[k] * a.scale_log2e : -INFINITY;
+        z[k] = lane + G * k <= last ? (FB ? bf16r(z[k] * a.scale) : z[k] * a.scale_log2e) : -INFINITY;
         m = fmaxf(m, z[k]);
     }
     m = group_max<G>(m);
     float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < NM; ++k) {
-        z[k] = __builtin_amdgcn_exp2f(z[k] - m);  // masked slots: exp2(-inf) = 0
+        z[k] = FB ? fb_exp(z[k], m) : __builtin_amdgcn_exp2f(z[k] - m);  // masked slots: exp2(-inf) = 0
         s += z[k];
     }
     s = group_sum<G>(s);
     const float inv = 1.0f / s;
+    const float den = bf16r(s);
     const int full = a.cols / G;  // slots [0, full) hold a valid element in every lane
     auto store_all = [&](auto odt_tag) {
         constexpr int ODT = decltype(odt_tag)::value;
         if (!valid) return;
 #pragma unroll
         for (int k = 0; k < NM; ++k) {
-            if (k < full || lane + G * k <= last) st1<ODT, MBRT_NT_SMR>(a.out, base + lane + G * k, z[k] * inv);
+            if (k < full || lane + G * k <= last)
+                st1<ODT, MBRT_NT_SMR>(a.out, base + lane + G * k, FB ? bf16r(z[k] / den) : z[k] * inv);
         }
     };
     with_dt(a.odt, store_all);
@@ -86,7 +95,7 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(SmArgs a) {
 // as above but fed from LDS, writing the probabilities back over their inputs, phase 3
 // stores the span.  In-place calls are safe: the whole span is in LDS before its first
 // store.
-template <int IDT, int ODT, int G, int NM, int RPG>
+template <int IDT, int ODT, int G, int NM, int RPG, bool FB>
 __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
     constexpr int RB = RPG * kThreads / G;
     // rows of more than 128 elements (groups of 32 or 64 lanes) have their own cache policy
@@ -188,22 +197,23 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
         for (int k = 0; k < NM; ++k) {
             const int e = slot(k);
             const float x = get(rbase + (kRot ? e : min(e, last)));
-            z[k] = e <= last ? x * a.scale_log2e : -INFINITY;
+            z[k] = e <= last ? (FB ? bf16r(x * a.scale) : x * a.scale_log2e) : -INFINITY;
             m = fmaxf(m, z[k]);
         }
         m = group_max<G>(m);
         float s = 0.0f;
 #pragma unroll
         for (int k = 0; k < NM; ++k) {
-            z[k] = __builtin_amdgcn_exp2f(z[k] - m);
+            z[k] = FB ? fb_exp(z[k], m) : __builtin_amdgcn_exp2f(z[k] - m);
             s += z[k];
         }
         s = group_sum<G>(s);
         const float inv = 1.0f / s;
+        const float den = bf16r(s);
         if (r < nrows) {
 #pragma unroll
             for (int k = 0; k < NM; ++k)
-                if (slot(k) <= last) put(rbase + slot(k), z[k] * inv);
+                if (slot(k) <= last) put(rbase + slot(k), FB ? bf16r(z[k] / den) : z[k] * inv);
         }
     }
     __syncthreads();
@@ -228,11 +238,22 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
 }
 
 // Long rows: one wave per row, three passes (max, sum, write) over global memory.
-__global__ __launch_bounds__(kThreads) void softmax_loop_kernel(SmArgs a, int idt) {
+__global__ __launch_bounds__(kThreads) void softmax_loop_kernel(SmArgs a, int idt, int fb) {
     const int lane = threadIdx.x % 64;
     const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
     if (row >= a.rows) return;
     const int64_t start = row * a.cols;
+    if (fb) {
+        float m = -INFINITY;
+        for (int64_t c = lane; c < a.cols; c += 64) m = fmaxf(m, bf16r(load1(a.in, idt, start + c) * a.scale));
+        m = group_max<64>(m);
+        float s = 0.0f;
+        for (int64_t c = lane; c < a.cols; c += 64) s += fb_exp(bf16r(load1(a.in, idt, start + c) * a.scale), m);
+        const float den = bf16r(group_sum<64>(s));
+        for (int64_t c = lane; c < a.cols; c += 64)
+            store1(a.out, a.odt, start + c, bf16r(fb_exp(bf16r(load1(a.in, idt, start + c) * a.scale), m) / den));
+        return;
+    }
     float m = -INFINITY;
     for (int64_t c = lane; c < a.cols; c += 64) m = fmaxf(m, load1(a.in, idt, start + c) * a.scale_log2e);
     m = group_max<64>(m);
@@ -247,10 +268,17 @@ __global__ __launch_bounds__(kThreads) void softmax_loop_kernel(SmArgs a, int id
 }
 
 template <int IDT, int G, int NM, int RPG = 1>
-void launch_staged(const SmArgs& a, hipStream_t st) {
+void launch_staged(const SmArgs& a, bool fb, hipStream_t st) {
+    const dim3 grid((unsigned)ceil_div(a.rows, RPG * kThreads / G));
+    if constexpr (IDT == BF16) {
+        if (fb) {
+            hipLaunchKernelGGL((softmax_staged_kernel<BF16, BF16, G, NM, RPG, true>), grid, dim3(kThreads), 0, st, a);
+            return;
+        }
+    }
     with_dt(a.odt, [&](auto ot) {
-        hipLaunchKernelGGL((softmax_staged_kernel<IDT, decltype(ot)::value, G, NM, RPG>),
-                           dim3((unsigned)ceil_div(a.rows, RPG * kThreads / G)), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((softmax_staged_kernel<IDT, decltype(ot)::value, G, NM, RPG, false>), grid, dim3(kThreads),
+                           0, st, a);
     });
 }
 
@@ -259,7 +287,7 @@ void launch_staged(const SmArgs& a, hipStream_t st) {
 // groups (many rows per block); rows of 129..1024 use 64 lanes per row (4 rows per block)
 // or, when 4 rows do not fill whole vectors (bf16 rows of odd length), 32 lanes (8 rows).
 template <int IDT>
-bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) {
+bool launch_short(const SmArgs& a, int in_esize, int out_esize, bool fb, hipStream_t st) {
     const int c = a.cols;
     if (c > 1024 || !aligned(a.in, 16) || !aligned(a.out, 16)) return false;
     auto fits = [&](int rb) {
@@ -271,24 +299,24 @@ bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) 
     // MBRT_SM_SHORT_BYTES of input its fixed cost dominates, so each group takes
     // MBRT_SM_SHORT_RPG rows
     const bool two = 32 * c * in_esize < MBRT_SM_SHORT_BYTES;
-    if (c <= 16 && fits(64)) launch_staged<IDT, 4, 4>(a, st);
-    else if (c <= 32 && fits(32)) launch_staged<IDT, 8, 4>(a, st);
-    else if (c <= 64 && two && fits(32 * MBRT_SM_SHORT_RPG)) launch_staged<IDT, 8, 8, MBRT_SM_SHORT_RPG>(a, st);
-    else if (c <= 64 && fits(32)) launch_staged<IDT, 8, 8>(a, st);
-    else if (c <= 128 && fits(16)) launch_staged<IDT, 16, 8>(a, st);
+    if (c <= 16 && fits(64)) launch_staged<IDT, 4, 4>(a, fb, st);
+    else if (c <= 32 && fits(32)) launch_staged<IDT, 8, 4>(a, fb, st);
+    else if (c <= 64 && two && fits(32 * MBRT_SM_SHORT_RPG)) launch_staged<IDT, 8, 8, MBRT_SM_SHORT_RPG>(a, fb, st);
+    else if (c <= 64 && fits(32)) launch_staged<IDT, 8, 8>(a, fb, st);
+    else if (c <= 128 && fits(16)) launch_staged<IDT, 16, 8>(a, fb, st);
     else if (c <= 128 || !MBRT_SM_STAGE_LONG) return false;
     else if (MBRT_SM_LONG_G == 64 && fits(4 * MBRT_SM_LONG_RPG)) {
         constexpr int R = MBRT_SM_LONG_RPG;
-        if (c <= 256) launch_staged<IDT, 64, 4, R>(a, st);
-        else if (c <= 512) launch_staged<IDT, 64, 8, R>(a, st);
-        else if (c <= 832) launch_staged<IDT, 64, 13, R>(a, st);
-        else launch_staged<IDT, 64, 16, R>(a, st);
+        if (c <= 256) launch_staged<IDT, 64, 4, R>(a, fb, st);
+        else if (c <= 512) launch_staged<IDT, 64, 8, R>(a, fb, st);
+        else if (c <= 832) launch_staged<IDT, 64, 13, R>(a, fb, st);
+        else launch_staged<IDT, 64, 16, R>(a, fb, st);
     } else if (fits(8 * MBRT_SM_LONG_RPG)) {
         constexpr int R = MBRT_SM_LONG_RPG;
-        if (c <= 256) launch_staged<IDT, 32, 8, R>(a, st);
-        else if (c <= 512) launch_staged<IDT, 32, 16, R>(a, st);
-        else if (c <= 832) launch_staged<IDT, 32, 26, R>(a, st);
-        else launch_staged<IDT, 32, 32, R>(a, st);
+        if (c <= 256) launch_staged<IDT, 32, 8, R>(a, fb, st);
+        else if (c <= 512) launch_staged<IDT, 32, 16, R>(a, fb, st);
+        else if (c <= 832) launch_staged<IDT, 32, 26, R>(a, fb, st);
+        else launch_staged<IDT, 32, 32, R>(a, fb, st);
     } else {
         return false;
     }
@@ -296,26 +324,32 @@ bool launch_short(const SmArgs& a, int in_esize, int out_esize, hipStream_t st) 
 }
 
 template <int IDT, int G, int NM>
-void launch_rows(const SmArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((softmax_rows_kernel<IDT, G, NM>), dim3((unsigned)ceil_div(a.rows, kThreads / G)),
-                       dim3(kThreads), 0, st, a);
+void launch_rows(const SmArgs& a, bool fb, hipStream_t st) {
+    const dim3 grid((unsigned)ceil_div(a.rows, kThreads / G));
+    if constexpr (IDT == BF16) {
+        if (fb) {
+            hipLaunchKernelGGL((softmax_rows_kernel<IDT, G, NM, true>), grid, dim3(kThreads), 0, st, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((softmax_rows_kernel<IDT, G, NM, false>), grid, dim3(kThreads), 0, st, a);
 }
 
 // Picks the group width and slots per lane for a row length; false when too long.
 template <int IDT>
-bool launch_fast(const SmArgs& a, hipStream_t st) {
+bool launch_fast(const SmArgs& a, bool fb, hipStream_t st) {
     const int c = a.cols;
-    if (c <= 8) launch_rows<IDT, 8, 1>(a, st);
-    else if (c <= 16) launch_rows<IDT, 16, 1>(a, st);
-    else if (c <= 32) launch_rows<IDT, 16, 2>(a, st);
-    else if (c <= 64) launch_rows<IDT, 16, 4>(a, st);
-    else if (c <= 128) launch_rows<IDT, 32, 4>(a, st);
-    else if (c <= 256) launch_rows<IDT, 64, 4>(a, st);
-    else if (c <= 512) launch_rows<IDT, 64, 8>(a, st);
-    else if (c <= 832) launch_rows<IDT, 64, 13>(a, st);
-    else if (c <= 1024) launch_rows<IDT, 64, 16>(a, st);
-    else if (c <= 1344) launch_rows<IDT, 64, 21>(a, st);
-    else if (c <= 2048) launch_rows<IDT, 64, 32>(a, st);
+    if (c <= 8) launch_rows<IDT, 8, 1>(a, fb, st);
+    else if (c <= 16) launch_rows<IDT, 16, 1>(a, fb, st);
+    else if (c <= 32) launch_rows<IDT, 16, 2>(a, fb, st);
+    else if (c <= 64) launch_rows<IDT, 16, 4>(a, fb, st);
+    else if (c <= 128) launch_rows<IDT, 32, 4>(a, fb, st);
+    else if (c <= 256) launch_rows<IDT, 64, 4>(a, fb, st);
+    else if (c <= 512) launch_rows<IDT, 64, 8>(a, fb, st);
+    else if (c <= 832) launch_rows<IDT, 64, 13>(a, fb, st);
+    else if (c <= 1024) launch_rows<IDT, 64, 16>(a, fb, st);
+    else if (c <= 1344) launch_rows<IDT, 64, 21>(a, fb, st);
+    else if (c <= 2048) launch_rows<IDT, 64, 32>(a, fb, st);
     else return false;
     return true;
 }
@@ -343,15 +377,18 @@ int mbrt_softmax_rows(const void* in, int in_dtype, void* out, int out_dtype, in
     a.rows = rows;
     a.cols = (int)cols;
     a.scale_log2e = scale * kLog2e;
+    a.scale = scale;
+    // bf16 intermediates: bf16 -> bf16 rows, as in the reference
+    const bool fb = bf16_intermediates() && in_dtype == BF16 && out_dtype == BF16;
     hipStream_t st = as_stream(stream);
     const int ies = dt_size(in_dtype), oes = dt_size(out_dtype);
     bool done;
-    if (in_dtype == F32) done = launch_short<F32>(a, ies, oes, st) || launch_fast<F32>(a, st);
-    else if (in_dtype == BF16) done = launch_short<BF16>(a, ies, oes, st) || launch_fast<BF16>(a, st);
-    else done = launch_short<F16>(a, ies, oes, st) || launch_fast<F16>(a, st);
+    if (in_dtype == F32) done = launch_short<F32>(a, ies, oes, false, st) || launch_fast<F32>(a, false, st);
+    else if (in_dtype == BF16) done = launch_short<BF16>(a, ies, oes, fb, st) || launch_fast<BF16>(a, fb, st);
+    else done = launch_short<F16>(a, ies, oes, false, st) || launch_fast<F16>(a, false, st);
     if (!done) {
         hipLaunchKernelGGL(softmax_loop_kernel, dim3((unsigned)ceil_div(rows, kThreads / 64)), dim3(kThreads), 0, st, a,
-                           in_dtype);
+                           in_dtype, fb ? 1 : 0);
     }
     return check_launch(op);
 }

@@ -4,8 +4,6 @@
 #include "mbr_tile.h"
 
 #include <algorithm>
-#include <atomic>
-#include <cstdio>
 #include <limits>
 #include <stdexcept>
 #include <string>
@@ -24,9 +22,7 @@ bool all_bf16_experiments() {
 bool remaining_bf16_experiments() {
     return g_quantize_bf16 && (custom_bf16_path() || env_flag_enabled("CUDASEP_REMAINING_BF16_EXPERIMENTS"));
 }
-void warn_full_bf16_arith();
 bool bf16_experiment(const char* name) {
-    warn_full_bf16_arith();
     return g_quantize_bf16 && (all_bf16_experiments() || env_flag_enabled(name));
 }
 bool remaining_bf16_experiment(const char* name) {
@@ -43,16 +39,25 @@ bool tanh_bf16_input() { return remaining_bf16_experiment("CUDASEP_TANH_BF16_INP
 bool freq_attention60_padded() {
     return g_quantize_bf16 && !env_flag_enabled("CUDASEP_DISABLE_FREQ_ATTENTION60_CUTILE_PADDED");
 }
-// CUDASEP_FULL_BF16_ARITH_EXPERIMENTS (src/mbr_cuda_tile.cu:190-192) rounds intermediate
-// values (sums of squares, row maxima, exponentials, ...) to bf16 inside the reference's
-// kernels.  This library does not build that experiment: the switch is not honoured, and
-// the first policy query under bf16 says so once on stderr instead of ignoring it silently.
-void warn_full_bf16_arith() {
-    static std::atomic<bool> warned{false};
-    if (!warned.load(std::memory_order_relaxed) && g_quantize_bf16 &&
-        env_flag_enabled("CUDASEP_FULL_BF16_ARITH_EXPERIMENTS") && !warned.exchange(true))
-        std::fprintf(stderr, "[mbr_tile] CUDASEP_FULL_BF16_ARITH_EXPERIMENTS is not supported; ignored\n");
-}
+// CUDASEP_FULL_BF16_ARITH_EXPERIMENTS under bf16 (full_bf16_arith_enabled,
+// src/mbr_cuda_tile.cu:190-192): the reference's kernels then round intermediates (sums of
+// squares, row maxima, exponentials, gates, ...) to bf16.  The ops that take the mode hold
+// this scope around their C-ABI call, which sets MBRT_ARITH_BF16_INTERMEDIATES on the
+// calling thread exactly while the switch is on, and restores the caller's flags after.
+class FullBf16Scope {
+public:
+    FullBf16Scope() : prev_(mbrt_get_arith_flags()) {
+        const bool on = g_quantize_bf16 && env_flag_enabled("CUDASEP_FULL_BF16_ARITH_EXPERIMENTS");
+        const uint32_t want = on ? (prev_ | MBRT_ARITH_BF16_INTERMEDIATES) : (prev_ & ~(uint32_t)MBRT_ARITH_BF16_INTERMEDIATES);
+        if (want != prev_) mbrt_set_arith_flags(want);
+    }
+    ~FullBf16Scope() { mbrt_set_arith_flags(prev_); }
+    FullBf16Scope(const FullBf16Scope&) = delete;
+    FullBf16Scope& operator=(const FullBf16Scope&) = delete;
+
+private:
+    uint32_t prev_;
+};
 
 constexpr int kFreqAttnN = 60;
 constexpr int kFreqAttnPadN = 64;
@@ -113,6 +118,7 @@ Tensor rms_norm(const Tensor& x, const Tensor& gamma, float scale) {
     const DType odt = rms_norm_bf16() ? DType::BFloat16 : f32_pipeline_out(xc.dtype());
     Tensor out = Tensor::empty(xc.shape(), odt);
     if (xc.numel() == 0) return out;
+    FullBf16Scope full_bf16;
     abi_check(mbrt_rms_norm(xc.data_ptr(), code(xc.dtype()), gf.data_ptr(), code(gf.dtype()), out.data_ptr(), code(odt),
                             xc.numel() / dim, dim, scale, 1e-12f, abi_stream()),
               "mbr_tile::rms_norm");
@@ -131,6 +137,7 @@ bool try_residual_add_rms_norm(const Tensor& residual, const Tensor& update, con
     const DType ndt = rms_norm_bf16() ? DType::BFloat16 : f32_pipeline_out(residual.dtype());
     Tensor sum = Tensor::empty(residual.shape(), residual.dtype());
     Tensor out = Tensor::empty(residual.shape(), ndt);
+    FullBf16Scope full_bf16;
     abi_check(mbrt_residual_add_rms_norm(residual.data_ptr(), update.data_ptr(), code(residual.dtype()), gf.data_ptr(),
                                          code(gf.dtype()), sum.data_ptr(), code(residual.dtype()), out.data_ptr(),
                                          code(ndt), residual.numel() / dim, dim, scale, 1e-12f, abi_stream()),
@@ -162,6 +169,7 @@ void split_qkv_heads_rotary(const Tensor& qkv, int heads, int dim_head, const Te
     k = Tensor::empty({B, (int64_t)heads, out_n, (int64_t)dim_head}, odt);
     v = Tensor::empty({B, (int64_t)heads, out_n, (int64_t)dim_head}, odt);
     if (x.numel() == 0) return;
+    FullBf16Scope full_bf16;
     abi_check(mbrt_split_qkv_heads_rotary(x.data_ptr(), code(x.dtype()), c.data_ptr(), s.data_ptr(), code(c.dtype()),
                                           q.data_ptr(), k.data_ptr(), v.data_ptr(), code(odt), B, N, heads, dim_head,
                                           out_n, abi_stream()),
@@ -183,6 +191,7 @@ void rotary_inplace(Tensor& q, Tensor* k, const Tensor& cos_freqs, const Tensor&
     const Tensor c = f32_or_bf16(cos_freqs), s = f32_or_bf16(sin_freqs);
     if (c.dtype() != s.dtype()) throw std::runtime_error(std::string(op) + ": cos/sin dtypes differ");
     if (q.numel() == 0) return;
+    FullBf16Scope full_bf16;
     abi_check(mbrt_rotary_inplace(q.data_ptr(), k ? k->data_ptr() : nullptr, code(q.dtype()), c.data_ptr(),
                                   s.data_ptr(), code(c.dtype()), q.numel() / D, N, H, D, MBRT_LAYOUT_BNHD,
                                   abi_stream()),
@@ -208,6 +217,7 @@ Tensor gate_merge(const Tensor& attn, const Tensor& gates, int heads, int dim_he
     const DType odt = gate_merge_bf16() ? DType::BFloat16 : DType::Float32;
     Tensor merged = Tensor::empty({B, N, (int64_t)heads * dim_head}, odt);
     if (merged.numel() == 0) return merged;
+    FullBf16Scope full_bf16;
     abi_check(mbrt_sigmoid_gate_merge(a.data_ptr(), code(a.dtype()), g.data_ptr(), code(g.dtype()), logits ? 1 : 0,
                                       merged.data_ptr(), code(odt), B, heads, N, dim_head, MBRT_LAYOUT_BHND,
                                       abi_stream()),
@@ -294,6 +304,7 @@ Tensor softmax_last_dim(const Tensor& x, float scale, DType out_dtype) {
     Tensor out = Tensor::empty(xc.shape(), out_dtype);
     if (xc.numel() == 0) return out;
     const int64_t cols = xc.size(xc.ndim() - 1);
+    FullBf16Scope full_bf16;
     abi_check(mbrt_softmax_rows(xc.data_ptr(), code(xc.dtype()), out.data_ptr(), code(out_dtype), xc.numel() / cols,
                                 cols, scale, abi_stream()),
               "mbr_tile::softmax_last_dim");
@@ -304,6 +315,7 @@ void softmax_last_dim_(Tensor& x, float scale) {
     if (!x.is_contiguous()) throw std::runtime_error("mbr_tile::softmax_last_dim_: expected a contiguous tensor");
     if (x.numel() == 0) return;
     const int64_t cols = x.size(x.ndim() - 1);
+    FullBf16Scope full_bf16;
     abi_check(mbrt_softmax_rows(x.data_ptr(), code(x.dtype()), x.data_ptr(), code(x.dtype()), x.numel() / cols, cols,
                                 scale, abi_stream()),
               "mbr_tile::softmax_last_dim_");
@@ -348,6 +360,7 @@ Tensor glu_last_dim(const Tensor& x) {
     shape.back() = full / 2;
     Tensor out = Tensor::empty(shape, odt);
     if (out.numel() == 0) return out;
+    FullBf16Scope full_bf16;
     abi_check(mbrt_glu_last_dim(xc.data_ptr(), code(xc.dtype()), out.data_ptr(), code(odt), xc.numel() / full,
                                 full / 2, abi_stream()),
               "glu_last_dim");
@@ -427,6 +440,7 @@ Tensor apply_mask_and_scatter(const Tensor& stft_repr, const std::vector<Tensor>
     Tensor out = Tensor::empty({batch * num_stems * audio_channels, total_freq / audio_channels, frames, 2}, odt);
     if (out.numel() == 0) return out;
     const void* mptr[2] = {masks[0].data_ptr(), masks[num_stems - 1].data_ptr()};
+    FullBf16Scope full_bf16;
     abi_check(mbrt_band_mask_merge((const float*)stft.data_ptr(), mptr, code(mdt), (int)num_stems, offsets.data_ptr(),
                                    indices.data_ptr(), MBRT_I64, counts.data_ptr(), code(counts.dtype()),
                                    out.data_ptr(), code(odt), batch, total_freq, frames, total_band_freqs,

@@ -12,7 +12,8 @@ import torch
 
 from . import _abi
 from ._abi import (  # noqa: F401
-    ACT_GELU_REF, ACT_GELU_STD, ACT_NONE, ACT_SIGMOID, ACT_TANH, ADD, BF16, DIV, F16, F32, I32, I64,
+    ACT_GELU_REF, ACT_GELU_STD, ACT_NONE, ACT_SIGMOID, ACT_TANH, ADD, ARITH_BF16_INTERMEDIATES, BF16, DIV, F16, F32,
+    I32, I64,
     LAYOUT_BHND, LAYOUT_BNHD, MUL, REDUCE_MAX, REDUCE_SUM, SCALAR_ADD, SCALAR_CLAMP, SCALAR_MUL, SUB,
     UNARY_GT, UNARY_NEG, MbrtError, lib, LIB_PATH,
 )
@@ -49,6 +50,32 @@ def version() -> int:
 
 def sync(stream=None) -> None:
     _abi.call("mbrt_stream_sync", _s(stream))
+
+
+def get_arith_flags() -> int:
+    return int(lib().mbrt_get_arith_flags())
+
+
+def set_arith_flags(flags: int) -> None:
+    """Arithmetic flags for later calls from this thread (ARITH_BF16_INTERMEDIATES: the
+    reference's full-bf16 experiment mode, src/mbr_cuda_tile.cu:190-192)."""
+    _abi.call("mbrt_set_arith_flags", int(flags))
+
+
+class arith_flags:
+    """Context manager: `with mbrt.arith_flags(mbrt.ARITH_BF16_INTERMEDIATES): ...`"""
+
+    def __init__(self, flags: int):
+        self.flags = flags
+
+    def __enter__(self):
+        self.prev = get_arith_flags()
+        set_arith_flags(self.flags)
+        return self
+
+    def __exit__(self, *exc):
+        set_arith_flags(self.prev)
+        return False
 
 
 # ---- tensor library --------------------------------------------------------------------

@@ -22,6 +22,8 @@ UNARY_NEG, UNARY_GT = 0, 1
 REDUCE_SUM, REDUCE_MAX = 0, 1
 ACT_NONE, ACT_GELU_REF, ACT_GELU_STD, ACT_SIGMOID, ACT_TANH = 0, 1, 2, 3, 4
 LAYOUT_BHND, LAYOUT_BNHD = 0, 1
+# arithmetic flags (mbrt_set_arith_flags)
+ARITH_BF16_INTERMEDIATES = 1
 
 STATUS_NAMES = {
     0: "MBRT_OK",
@@ -70,6 +72,8 @@ SIGNATURES: dict[str, list] = {
     "mbrt_last_error": [],
     "mbrt_version": [],
     "mbrt_stream_sync": [P],
+    "mbrt_set_arith_flags": [C.c_uint32],
+    "mbrt_get_arith_flags": [],
     "mbrt_fill": [P, I, L, D, P],
     "mbrt_arange": [P, I, L, L, P],
     "mbrt_convert": [P, I, P, I, L, P],
@@ -114,6 +118,7 @@ SIGNATURES: dict[str, list] = {
 }
 _RESTYPE = {
     "mbrt_last_error": C.c_char_p,
+    "mbrt_get_arith_flags": C.c_uint32,
     "mbrt_stft_num_frames": C.c_int64,
     "mbrt_istft_output_length": C.c_int64,
     "mbrt_istft_workspace_bytes": C.c_int64,

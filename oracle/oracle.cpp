@@ -119,6 +119,10 @@ inline void st(void* p, int dt, int64_t i, float v) {
         default: static_cast<int32_t*>(p)[i] = (int32_t)v; break;
     }
 }
+// One rounding of a double to the nearest bf16, widened back: an intermediate of the
+// bf16-intermediates mode (the reference's bf16_round in full-bf16 mode).
+inline double rb(double v) { return (double)bf16_to_f32(f64_to_bf16(v)); }
+
 inline float round_through(float v, int dt) {
     if (dt == BF16) return bf16_to_f32(f32_to_bf16(v));
     if (dt == F16) return f16_to_f32(f32_to_f16(v));
@@ -381,7 +385,14 @@ void orc_rms_norm(const void* x, int xdt, const void* res, const void* gamma, in
             }
             s[d] = v;
         }
-        if (mode == ORC_EXACT) {
+        if (mode == ORC_BF16I) {
+            // src/mbr_cuda_tile.cu:4830-4843, 4890-4905
+            double ss = 0;
+            for (int64_t d = 0; d < dim; ++d) ss += rb(s[d]) * rb(s[d]);
+            const double inv = rb(1.0 / std::sqrt(rb(ss) + (double)eps));
+            for (int64_t d = 0; d < dim; ++d)
+                st(out, odt, base + d, rb(rb(s[d]) * inv * rb(ld(gamma, gdt, d)) * (double)scale));
+        } else if (mode == ORC_EXACT) {
             double ss = 0;
             for (int64_t d = 0; d < dim; ++d) ss += (double)s[d] * s[d];
             const double inv = 1.0 / std::sqrt(ss + (double)eps);
@@ -422,7 +433,9 @@ void orc_glu(const void* x, int xdt, void* out, int odt, int64_t rows, int64_t h
     for (int64_t r = 0; r < rows; ++r) {
         for (int64_t d = 0; d < half; ++d) {
             const int64_t i = r * 2 * half + d;
-            if (mode == ORC_EXACT)
+            if (mode == ORC_BF16I)  // src/mbr_cuda_tile.cu:5933-5938
+                st(out, odt, r * half + d, rb(rb(ld(x, xdt, i)) * rb(sigmoid<double>(rb(ld(x, xdt, i + half))))));
+            else if (mode == ORC_EXACT)
                 st(out, odt, r * half + d, (double)ld(x, xdt, i) * sigmoid<double>(ld(x, xdt, i + half)));
             else
                 st(out, odt, r * half + d, ld(x, xdt, i) * sigmoid<float>(ld(x, xdt, i + half)));
@@ -444,7 +457,9 @@ void orc_gate_merge(const void* attn, int adt, const void* gate, int gdt, int lo
             for (int64_t d = 0; d < D; ++d) {
                 const int64_t src = layout == 0 ? ((b * H + h) * N + n) * D + d : (tok * H + h) * D + d;
                 const int64_t dst = (tok * H + h) * D + d;
-                if (mode == ORC_EXACT) st(out, odt, dst, (double)ld(attn, adt, src) * gd);
+                if (mode == ORC_BF16I)  // src/mbr_cuda_tile.cu:4743-4746
+                    st(out, odt, dst, rb(rb(ld(attn, adt, src)) * rb(gd)));
+                else if (mode == ORC_EXACT) st(out, odt, dst, (double)ld(attn, adt, src) * gd);
                 else st(out, odt, dst, ld(attn, adt, src) * gf);
             }
         }
@@ -456,7 +471,20 @@ void orc_softmax(const void* in, int idt, void* out, int odt, int64_t rows, int6
 #pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t r = 0; r < rows; ++r) {
         const int64_t base = r * cols;
-        if (mode == ORC_EXACT) {
+        if (mode == ORC_BF16I) {
+            // src/mbr_cuda_tile.cu:5237-5248
+            std::vector<double> z(cols);
+            double m = -INFINITY;
+            for (int64_t c = 0; c < cols; ++c) {
+                z[c] = rb(rb(ld(in, idt, base + c)) * (double)scale);
+                m = std::max(m, z[c]);
+            }
+            m = rb(m);
+            double s = 0;
+            for (int64_t c = 0; c < cols; ++c) s += (z[c] = rb(std::exp(z[c] - m)));
+            const double den = rb(s);
+            for (int64_t c = 0; c < cols; ++c) st(out, odt, base + c, rb(z[c] / den));
+        } else if (mode == ORC_EXACT) {
             std::vector<double> z(cols);
             double m = -INFINITY;
             for (int64_t c = 0; c < cols; ++c) {
@@ -504,13 +532,22 @@ void orc_rotary(void* q, void* k, int dt, const void* cos_t, const void* sin_t, 
     for (int64_t r = 0; r < rows; ++r) {
         const int64_t n = (layout == 1 ? r / heads : r) % n_pos;
         for (int64_t i = 0; i < half; ++i) {
-            const float c = ld(cos_t, tdt, n * half + i), s = ld(sin_t, tdt, n * half + i);
+            float c = ld(cos_t, tdt, n * half + i), s = ld(sin_t, tdt, n * half + i);
+            if (mode == ORC_BF16I) {  // src/mbr_cuda_tile.cu:4033-4060 (and its in-place variants)
+                c = (float)rb(c);
+                s = (float)rb(s);
+            }
             for (int t = 0; t < 2; ++t) {
                 void* buf = t == 0 ? q : k;
                 if (!buf) continue;
                 const int64_t e = r * D + 2 * i;
-                const float x0 = ld(buf, dt, e), x1 = ld(buf, dt, e + 1);
-                if (mode == ORC_EXACT) {
+                float x0 = ld(buf, dt, e), x1 = ld(buf, dt, e + 1);
+                if (mode == ORC_BF16I) {
+                    x0 = (float)rb(x0);
+                    x1 = (float)rb(x1);
+                    st(buf, dt, e, rb((double)x0 * c - (double)x1 * s));
+                    st(buf, dt, e + 1, rb((double)x0 * s + (double)x1 * c));
+                } else if (mode == ORC_EXACT) {
                     st(buf, dt, e, (double)x0 * c - (double)x1 * s);
                     st(buf, dt, e + 1, (double)x0 * s + (double)x1 * c);
                 } else {
@@ -540,13 +577,21 @@ void orc_split_qkv(const void* qkv, int idt, const void* cos_t, const void* sin_
                         continue;
                     }
                     const int64_t src = (b * N + n) * 3 * H * D + h * D + 2 * i;
-                    const float c = ld(cos_t, tdt, n * half + i), s = ld(sin_t, tdt, n * half + i);
+                    float c = ld(cos_t, tdt, n * half + i), s = ld(sin_t, tdt, n * half + i);
+                    if (mode == ORC_BF16I) {  // src/mbr_cuda_tile.cu:4033-4060
+                        c = (float)rb(c);
+                        s = (float)rb(s);
+                    }
                     for (int part = 0; part < 3; ++part) {
                         void* dst = part == 0 ? q : part == 1 ? k : v;
                         const float x0 = ld(qkv, idt, src + part * H * D), x1 = ld(qkv, idt, src + part * H * D + 1);
                         if (part == 2) {
                             st(dst, odt, e, x0);
                             st(dst, odt, e + 1, x1);
+                        } else if (mode == ORC_BF16I) {
+                            const double y0 = rb(x0), y1 = rb(x1);
+                            st(dst, odt, e, rb(y0 * c - y1 * s));
+                            st(dst, odt, e + 1, rb(y0 * s + y1 * c));
                         } else if (mode == ORC_EXACT) {
                             st(dst, odt, e, (double)x0 * c - (double)x1 * s);
                             st(dst, odt, e + 1, (double)x0 * s + (double)x1 * c);
@@ -663,7 +708,29 @@ void orc_band_mask_merge(const float* stft, const void* const* masks, int mdt, i
         for (int64_t t = 0; t < T; ++t) {
             const float* sv = stft + ((b * F + f) * T + t) * 2;
             const int64_t o = ((((b * S + s) * C + ch) * bins + bin) * T + t) * 2;
-            if (mode == ORC_EXACT) {
+            if (mode == ORC_BF16I && odt == BF16) {
+                // reduce form, src/mbr_cuda_tile.cu:5771-5799: sum the masks, rounding each sum
+                double mr = 0, mm = 0;
+                for (int32_t e = off[f]; e < off[f + 1]; ++e) {
+                    const int64_t mi = ((b * T + t) * J + ind[e]) * 2;
+                    mr = rb(mr + rb(ld(masks[s], mdt, mi)));
+                    mm = rb(mm + rb(ld(masks[s], mdt, mi + 1)));
+                }
+                st(out, odt, o, rb(((double)sv[0] * mr - (double)sv[1] * mm) / den));
+                st(out, odt, o + 1, rb(((double)sv[0] * mm + (double)sv[1] * mr) / den));
+            } else if (mode == ORC_BF16I) {
+                // scatter form, src/mbr_cuda_tile.cu:5702-5717: each entry's value is rounded,
+                // then added (here in ascending entry order)
+                double ar = 0, ai = 0;
+                for (int32_t e = off[f]; e < off[f + 1]; ++e) {
+                    const int64_t mi = ((b * T + t) * J + ind[e]) * 2;
+                    const double mr = rb(ld(masks[s], mdt, mi)), mm = rb(ld(masks[s], mdt, mi + 1));
+                    ar += rb(((double)sv[0] * mr - (double)sv[1] * mm) / den);
+                    ai += rb(((double)sv[0] * mm + (double)sv[1] * mr) / den);
+                }
+                st(out, odt, o, ar);
+                st(out, odt, o + 1, ai);
+            } else if (mode == ORC_EXACT) {
                 double ar = 0, ai = 0;
                 for (int32_t e = off[f]; e < off[f + 1]; ++e) {
                     const int64_t mi = ((b * T + t) * J + ind[e]) * 2;

@@ -10,7 +10,12 @@
  *   ORC_EXACT (0): compute in double, round once to the output dtype (round to nearest
  *                  even) — the "exact maths" value used for parity;
  *   ORC_FAST  (1): compute in float with the same operation order as the GPU kernels —
- *                  the loop that is timed as the CPU baseline.
+ *                  the loop that is timed as the CPU baseline;
+ *   ORC_BF16I (2): the reference's full-bf16 experiment mode: double arithmetic, rounded
+ *                  to bf16 at each point where the reference's bf16 kernels round under
+ *                  full_bf16 (rms_norm, softmax, glu, gate_merge, rotary, split_qkv,
+ *                  band_mask_merge; the cited kernel lines are at each op).  The caller
+ *                  picks the dtypes for which the reference takes those kernels.
  * Outer loops are OpenMP-parallel; orc_set_threads() picks the thread count.
  *
  * Each function cites the reference code whose semantics it restates
@@ -25,7 +30,7 @@
 extern "C" {
 #endif
 
-enum { ORC_EXACT = 0, ORC_FAST = 1 };
+enum { ORC_EXACT = 0, ORC_FAST = 1, ORC_BF16I = 2 };
 
 void orc_set_threads(int n);
 int orc_get_threads(void);

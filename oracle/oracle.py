@@ -19,7 +19,7 @@ HERE = Path(__file__).resolve().parent
 LIB = HERE / "liboracle.so"
 
 F32, F16, I64, BF16, I32 = 0, 1, 2, 3, 4
-EXACT, FAST = 0, 1
+EXACT, FAST, BF16I = 0, 1, 2
 
 _NP = {F32: np.float32, F16: np.uint16, BF16: np.uint16, I64: np.int64, I32: np.int32}
 

@@ -8,6 +8,7 @@
 //                               with the oracle.
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <functional>
@@ -17,6 +18,7 @@
 #include <string>
 #include <vector>
 
+#include "../../include/mbrt.h"
 #include "hip_context.h"
 #include "mbr_tile.h"
 #include "stft_tile.h"
@@ -392,6 +394,21 @@ void ops(const std::string& path) {
     d.save("split_q", sq);
     d.save("split_k", sk);
     d.save("split_v", sv);
+    {
+        // CUDASEP_FULL_BF16_ARITH_EXPERIMENTS under bf16: these ops round their
+        // intermediates to bf16 while they run and leave the thread's C-ABI flags as found
+        setenv("CUDASEP_FULL_BF16_ARITH_EXPERIMENTS", "1", 1);
+        d.save("full_rms_norm", M::rms_norm(I["x"], I["gamma"], scale));
+        d.save("full_glu", M::glu_last_dim(I["g"]));
+        d.save("full_softmax", M::softmax_last_dim(I["scores"].to_bf16(), 0.125f, DType::BFloat16));
+        d.save("full_gate_logits_merge", M::apply_gate_logits_and_merge_heads(I["attn"], I["logits"], 8, 64));
+        d.save("full_merge", M::apply_mask_and_scatter(I["stft"], {I["mask0"], I["mask1"]}, I["freq_indices"],
+                                                       I["csr_off"], I["csr_ind"], I["counts"], I["stft"].size(0), 2,
+                                                       I["stft"].size(1), I["freq_indices"].numel(),
+                                                       I["stft"].size(2), 2));
+        unsetenv("CUDASEP_FULL_BF16_ARITH_EXPERIMENTS");
+        if (mbrt_get_arith_flags() != 0) throw std::runtime_error("mbr_tile left the bf16-intermediates flag set");
+    }
     {
         namespace S = cudasep::stft_tile;
         const Tensor hann = S::hann_window(2048);

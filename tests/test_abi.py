@@ -45,7 +45,7 @@ def test_binding_covers_header():
 
 
 def test_version(lib):
-    assert lib.mbrt_version() == 10000
+    assert lib.mbrt_version() == 10100
 
 
 def test_header_is_c99(tmp_path):
@@ -57,7 +57,23 @@ def test_header_is_c99(tmp_path):
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", f"-I{REPO / 'include'}",
                     str(src), "-o", str(exe), f"-L{LIB.parent}", "-lmbrt", f"-Wl,-rpath,{LIB.parent}"], check=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True)
-    assert r.returncode == 0 and r.stdout.strip() == "10000"
+    assert r.returncode == 0 and r.stdout.strip() == "10100"
+
+
+def test_arith_flags_are_per_thread_and_validated(lib):
+    import threading
+
+    import mbrt
+
+    seen = []
+    with mbrt.arith_flags(mbrt.ARITH_BF16_INTERMEDIATES):
+        t = threading.Thread(target=lambda: seen.append(mbrt.get_arith_flags()))
+        t.start()
+        t.join()
+        assert mbrt.get_arith_flags() == mbrt.ARITH_BF16_INTERMEDIATES
+    assert seen == [0] and mbrt.get_arith_flags() == 0
+    assert lib.mbrt_set_arith_flags(0x80) == 1 and "unknown flags" in _err(lib)
+    assert mbrt.get_arith_flags() == 0
 
 
 def _err(lib) -> str:

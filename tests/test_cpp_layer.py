@@ -188,6 +188,27 @@ def test_mbr_tile_ops_match_oracle(orc, dev, tmp_path):
                                                                    logit=False), BF16, "gate merge")
     assert_close(_read(tmp_path, "gate_logits_merge")[1], orc.gate_merge(attn, BF16, logits, F32, BF16, B, H, N, Dh,
                                                                          logit=True), BF16, "gate logits merge")
+    # CUDASEP_FULL_BF16_ARITH_EXPERIMENTS: the oracle's bf16-intermediates mode, within the
+    # rule of tests/test_gpu_bf16i.py (2 bf16 ulps, 98 % identical; the merge's f32 scatter
+    # form to 2^-7 of its summed magnitude)
+    from test_gpu_bf16i import assert_bf16i
+    BF16I = 2
+    assert_bf16i(_read(tmp_path, "full_rms_norm")[1], orc.rms_norm(x, F32, gamma, F32, BF16, scale, 1e-12, mode=BF16I),
+                 BF16, "full-bf16 rms_norm")
+    assert_bf16i(_read(tmp_path, "full_glu")[1], orc.glu(g, BF16, BF16, mode=BF16I), BF16, "full-bf16 glu")
+    sb = orc.from_f32(scores, BF16)
+    assert_bf16i(_read(tmp_path, "full_softmax")[1], orc.softmax(sb, BF16, BF16, 0.125, mode=BF16I), BF16,
+                 "full-bf16 softmax")
+    assert_bf16i(_read(tmp_path, "full_gate_logits_merge")[1],
+                 orc.gate_merge(attn, BF16, logits, F32, BF16, B, H, N, Dh, logit=True, mode=BF16I), BF16,
+                 "full-bf16 gate logits merge", max_ulp=1.0, min_exact=0.99)
+    mb16 = [orc.from_f32(m, BF16) for m in (m0, m1)]
+    dt, y = _read(tmp_path, "full_merge")
+    assert dt == F32
+    ref_fm = orc.band_mask_merge(stft, [m.reshape(Bb, T, J, 2) for m in mb16], BF16, mb["csr_offsets"],
+                                 mb["csr_indices"], cnt, F32, F32, Bb, F, T, 2, mode=BF16I)
+    den_fm = merge_den(orc, stft, [orc.to_f32(m, BF16) for m in mb16], mb, Bb, F, T, 2)
+    assert float((np.abs(y.astype(np.float64) - ref_fm) / np.maximum(den_fm, 1e-30)).max()) <= 2.0 ** -7
     rq, rk = orc.rotary(q, k, BF16, cos, sin, F32, N, H, layout=1)
     assert_close(_read(tmp_path, "rot_q")[1], rq, BF16, "rotary q")
     assert_close(_read(tmp_path, "rot_k")[1], rk, BF16, "rotary k")
