@@ -85,7 +85,18 @@ struct AttnArgs {
     const void* gate;   // gate [B, n_q, H] of dtype gdt, or NULL: out [BH, n_q, 64]
     int gdt;
     int glogit;         // the gate holds logits: sigmoid(gate) multiplies
+    uint32_t nbh;       // B * H (the persistent form walks heads blockIdx.x, + gridDim.x, ...)
 };
+
+// Barrier for data that arrived by direct-to-LDS loads: the caller has waited (vmcnt) for
+// this wave's own loads, and the barrier makes every wave's visible.  Unlike
+// __syncthreads() it carries no memory fence, which would also wait for the previous
+// head's output stores.  The empty asm statements keep LDS accesses on their side.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 // max of the 16 scores a lane holds for one 16-query sub-block (the file is built without
 // NaN semantics, so the maxima need no quieting and fold into v_max3)
@@ -126,6 +137,42 @@ __device__ __forceinline__ void lds_read_vt(const uint32_t (&ad)[4], bf16x8 (&va
         va[db] = __builtin_bit_cast(bf16x8, u32x4{r[2 * db].x, r[2 * db].y, r[2 * db + 1].x, r[2 * db + 1].y});
 }
 
+// 16-byte fragments of a swizzled [64][64] bf16 LDS tile, read in one asm block and completed
+// before the statement ends: the persistent form reads its K and Q tiles this way, so that
+// the compiler, which cannot tell one LDS buffer from another, does not wait for the next
+// head's loads in flight (vmcnt 0) before these reads.  f[i] is read at byte address
+// ad[i % NA] + 2048 (i / NA).
+template <int N, int NA>
+__device__ __forceinline__ void lds_read_frags(const uint32_t (&ad)[NA], bf16x8 (&f)[N]) {
+    static_assert((N == 8 && NA == 2) || (N == 2 && NA == 2), "K: 4 key blocks x 2 halves; Q: 2 halves");
+    u32x4 r[N];
+    if constexpr (N == 8) {
+        asm volatile(
+            "ds_read_b128 %0, %8\n\t"
+            "ds_read_b128 %1, %9\n\t"
+            "ds_read_b128 %2, %8 offset:2048\n\t"
+            "ds_read_b128 %3, %9 offset:2048\n\t"
+            "ds_read_b128 %4, %8 offset:4096\n\t"
+            "ds_read_b128 %5, %9 offset:4096\n\t"
+            "ds_read_b128 %6, %8 offset:6144\n\t"
+            "ds_read_b128 %7, %9 offset:6144\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+            : "v"(ad[0]), "v"(ad[1])
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_read_b128 %0, %2\n\t"
+            "ds_read_b128 %1, %3\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1])
+            : "v"(ad[0]), "v"(ad[1])
+            : "memory");
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) f[i] = __builtin_bit_cast(bf16x8, r[i]);
+}
+
 __device__ __forceinline__ float xor_sum(float x) {
     x += __shfl_xor(x, 16);
     return x + __shfl_xor(x, 32);
@@ -140,23 +187,34 @@ __device__ __forceinline__ float xor_sum(float x) {
 // MBRT_ATTN_P_BF16_FAST (P rounded once to bf16 under the lazy max, and the row sum formed
 // by the MFMA from the same rounded P, as a 17th block of V columns that are all 1: no
 // rescale on most tiles and no VALU row sum).
-template <int ODT, int QS, int PM>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBRT_ATTN_WPE))) void attention_kernel(AttnArgs a) {
+// HEADS: the persistent form for heads of at most 64 queries and 64 keys (the frequency
+// attention): a workgroup walks heads blockIdx.x, + gridDim.x, ..., and while it computes
+// one head the next head's K, V and Q tiles are already loading into the other LDS buffers,
+// so that the loads, the arithmetic and the output stores of consecutive heads overlap.  A
+// workgroup per head instead (the general form) runs load, arithmetic and store of its head
+// in turn, in step with every other workgroup on the CU.
+template <int ODT, int QS, int PM, bool HEADS>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(HEADS ? 3 : MBRT_ATTN_WPE))) void attention_kernel(AttnArgs a) {
     // two K and two V tiles: the next pair is loaded (straight into LDS) while the current
-    // one is read
+    // one is read; the persistent form also loads Q into LDS
     __shared__ __attribute__((aligned(16))) __bf16 k0[kKeys * kHeadDim];
     __shared__ __attribute__((aligned(16))) __bf16 v0[kKeys * kHeadDim];
     __shared__ __attribute__((aligned(16))) __bf16 k1[kKeys * kHeadDim];
     __shared__ __attribute__((aligned(16))) __bf16 v1[kKeys * kHeadDim];
+    constexpr int kQTile = HEADS ? kQBlock * kHeadDim : 8;
+    __shared__ __attribute__((aligned(16))) __bf16 qt0[kQTile];
+    __shared__ __attribute__((aligned(16))) __bf16 qt1[kQTile];
+    static_assert(!HEADS || QS == 1, "the persistent form holds 16 queries per wave");
     constexpr int kQB = kQWave * QS * kWaves;  // queries per workgroup
     const int tid = threadIdx.x;
     const int lane = tid % 64, g = lane / 16, c = lane % 16;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
     // one linear grid of (b, h, query tile), the query tiles of one (b, h) adjacent; each
     // XCD walks one contiguous range of it, so that the query tiles of a (b, h) run on one
-    // XCD, close in time, and read its K/V once into that XCD's L2
-    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
-    const uint32_t bh = tile / a.qtiles;
+    // XCD, close in time, and read its K/V once into that XCD's L2.  The persistent form
+    // starts at head blockIdx.x and has a single query tile.
+    const uint32_t tile = HEADS ? blockIdx.x : xcd_tile(blockIdx.x, gridDim.x);
+    uint32_t bh = tile / a.qtiles;
     const int q0 = (tile % a.qtiles) * kQB + w * kQWave * QS;
     uint32_t b, h;
     fdivmod(bh, a.heads, b, h);
@@ -164,14 +222,17 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBR
     const __bf16* vbase = a.v + b * a.kv_bs + h * a.kv_hs;
 
     // Q fragments: for sub-block x, lane holds Q[q0 + 16x + c][32s + 8g .. +7], s = 0, 1
+    // (the persistent form reads them from its LDS Q tile, head by head)
     bf16x8 qf[QS][2];
+    if constexpr (!HEADS) {
 #pragma unroll
     for (int x = 0; x < QS; ++x) {
         const __bf16* qrow = a.q + b * a.q_bs + h * a.q_hs + (int64_t)min(q0 + 16 * x + c, a.nq - 1) * a.q_rs;
 #pragma unroll
         for (int s = 0; s < 2; ++s) qf[x][s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
     }
-    if (a.cosp != nullptr) {
+    }
+    if (!HEADS && a.cosp != nullptr) {
         // in-kernel rotary of q: the lane's 8 values are the pairs 16s + 4g .. +3 of its query
         // row, rotated by the shared rotate() in f32 and rounded to bf16 as the rotary kernel
         // does (src/mbr_time_attention_cutile.cu:80-106, 489-490)
@@ -216,14 +277,17 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBR
     f32x4 o[QS][4];
     f32x4 osum[QS];  // kSumMfma: lane (g, c) holds the row sum of query c, four times
     float m[QS], l[QS];
+    auto reset_state = [&]() {
 #pragma unroll
-    for (int x = 0; x < QS; ++x) {
+        for (int x = 0; x < QS; ++x) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) o[x][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        osum[x] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        m[x] = -INFINITY;
-        l[x] = 0.0f;
-    }
+            for (int db = 0; db < 4; ++db) o[x][db] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            osum[x] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            m[x] = -INFINITY;
+            l[x] = 0.0f;
+        }
+    };
+    reset_state();
     // A operand of the row-sum MFMA: a 16 x 32 block of bf16 ones
     const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
@@ -264,31 +328,51 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBR
             __builtin_amdgcn_global_load_lds((global_void*)(vbase + off), (lds_void*)&vd[r0 * kHeadDim], 16, 0, 0);
         }
     };
-    load_tile(0, 0);
-    // One key tile: ks/vs hold it, kn/vn receive the next one.  The two buffer pairs are
-    // separate LDS objects and the loop below is unrolled by two, so the compiler sees that
-    // the loads in flight into kn/vn never alias the reads of ks/vs and waits for them only
-    // at the next tile's barrier.
-    auto tile_step = [&](int kt, const __bf16* ks, const __bf16* vs, int nbuf) {
-        // this wave's loads of the tile have landed (vmcnt 0); after the barrier every
-        // wave's have, and no wave still reads the other buffer, which is refilled next
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-        __syncthreads();
-        if (kt + kKeys < a.nk) load_tile(kt + kKeys, nbuf);
-        // a wave whose queries all lie past N (in the last query tile of a head) loads its
-        // share of every K/V tile and joins every barrier, but has nothing to compute
-        if (q0 >= a.nq) return;
-
+    // The persistent form's loads of one head (a single key tile and the query tile) into
+    // kd/vd/qd: wave w loads keys and queries 16w .. 16w + 15 as above, rows past n_k or
+    // n_q clamped.
+    auto load_head = [&](uint32_t hh, __bf16* kd, __bf16* vd, __bf16* qd) {
+        uint32_t hb, hh2;
+        fdivmod(hh, a.heads, hb, hh2);
+        const __bf16* kb = a.k + hb * a.kv_bs + hh2 * a.kv_hs;
+        const __bf16* vb = a.v + hb * a.kv_bs + hh2 * a.kv_hs;
+        const __bf16* qb = a.q + hb * a.q_bs + hh2 * a.q_hs;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int r0 = 16 * w + 8 * u, row = r0 + (lane >> 3);
+            const uint32_t chunk = 8 * ((lane & 7) ^ (lane >> 3));
+            const uint32_t koff = (uint32_t)min(row, a.nk - 1) * a.kv_rs + chunk;
+            const uint32_t qoff = (uint32_t)min(row, a.nq - 1) * a.q_rs + chunk;
+            __builtin_amdgcn_global_load_lds((global_void*)(kb + koff), (lds_void*)&kd[r0 * kHeadDim], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(vb + koff), (lds_void*)&vd[r0 * kHeadDim], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(qb + qoff), (lds_void*)&qd[r0 * kHeadDim], 16, 0, 0);
+        }
+    };
+    if constexpr (HEADS) load_head(bh, k0, v0, qt0);
+    else load_tile(0, 0);
+    // The arithmetic of one key tile held in ks/vs (below); the caller has made the tile
+    // visible to every wave.
+    auto tile_compute = [&](int kt, const __bf16* ks, const __bf16* vs) {
         // S^T = K Q^T for the 4 key blocks of the tile and every query sub-block
         if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
         f32x4 st[QS][4];
+        // the persistent form reads the tile's K fragments in one asm block (see
+        // lds_read_frags): kfr[2 kb + s] = K[16 kb + c][32 s + 8 g .. +7]
+        bf16x8 kfr[HEADS ? 8 : 1];
+        if constexpr (HEADS) {
+            const uint32_t kad[2] = {lds_addr(ks) + 2 * (uint32_t)tile_at(c, g, 0),
+                                     lds_addr(ks) + 2 * (uint32_t)tile_at(c, 4 + g, 0)};
+            lds_read_frags<8, 2>(kad, kfr);
+        }
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
             for (int x = 0; x < QS; ++x) st[x][kb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&ks[tile_at(16 * kb + c, 4 * s + g, 0)]);
+                bf16x8 ka;
+                if constexpr (HEADS) ka = kfr[2 * kb + s];
+                else ka = *reinterpret_cast<const bf16x8*>(&ks[tile_at(16 * kb + c, 4 * s + g, 0)]);
 #pragma unroll
                 for (int x = 0; x < QS; ++x)
                     st[x][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[x][s], st[x][kb], 0, 0, 0);
@@ -419,11 +503,24 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBR
             if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
         }
     };
-    for (int kt = 0; kt < a.nk; kt += 2 * kKeys) {
-        tile_step(kt, k0, v0, 1);
-        if (kt + kKeys < a.nk) tile_step(kt + kKeys, k1, v1, 0);
-    }
+    // One key tile: ks/vs hold it, kn/vn receive the next one.  The two buffer pairs are
+    // separate LDS objects and the loop below is unrolled by two, so the compiler sees that
+    // the loads in flight into kn/vn never alias the reads of ks/vs and waits for them only
+    // at the next tile's barrier.
+    auto tile_step = [&](int kt, const __bf16* ks, const __bf16* vs, int nbuf) {
+        // this wave's loads of the tile have landed (vmcnt 0); after the barrier every
+        // wave's have, and no wave still reads the other buffer, which is refilled next
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (kt + kKeys < a.nk) load_tile(kt + kKeys, nbuf);
+        // a wave whose queries all lie past N (in the last query tile of a head) loads its
+        // share of every K/V tile and joins every barrier, but has nothing to compute
+        if (q0 >= a.nq) return;
+        tile_compute(kt, ks, vs);
+    };
 
+    // the output of the head (b, h) = bh
+    auto store_out = [&]() {
 #pragma unroll
     for (int x = 0; x < QS; ++x) {
         const float lsum = kSumMfma ? osum[x][0] : xor_sum(l[x]);
@@ -465,6 +562,48 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(MBR
                 pk.y = pack_bf16x2(o[x][db][2] * inv, o[x][db][3] * inv);
                 *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + obase + d) = pk;
             }
+        }
+    }
+    };
+
+    if constexpr (!HEADS) {
+        for (int kt = 0; kt < a.nk; kt += 2 * kKeys) {
+            tile_step(kt, k0, v0, 1);
+            if (kt + kKeys < a.nk) tile_step(kt + kKeys, k1, v1, 0);
+        }
+        store_out();
+    } else {
+        // Head `cur` sits in ks/vs/qs; the next head of this workgroup loads into kn/vn/qn.
+        // Vector-memory operations retire in issue order, so when the previous head left
+        // exactly its kStores output stores behind the loads of `cur`, waiting until at most
+        // kStores are outstanding completes those loads and leaves the stores in flight.
+        // A wave without queries (q0 >= n_q) stores nothing and waits for all.
+        constexpr int kStores = 4;  // output stores per wave and head: one per 16-wide d block
+        bool first = true;
+        auto head_step = [&](uint32_t cur, const __bf16* ks, const __bf16* vs, const __bf16* qs, __bf16* kn,
+                             __bf16* vn, __bf16* qn) {
+            if (first || q0 >= a.nq) wait_vmcnt<0>();
+            else wait_vmcnt<kStores>();
+            first = false;
+            // every wave's loads of `cur` have landed, and no wave still reads kn/vn/qn
+            lds_barrier();
+            if (cur + gridDim.x < a.nbh) load_head(cur + gridDim.x, kn, vn, qn);
+            if (q0 >= a.nq) return;
+            bh = cur;
+            fdivmod(bh, a.heads, b, h);
+            // Q fragments of this wave's 16 queries from the swizzled LDS tile
+            const uint32_t qad[2] = {lds_addr(qs) + 2 * (uint32_t)tile_at(16 * w + c, g, 0),
+                                     lds_addr(qs) + 2 * (uint32_t)tile_at(16 * w + c, 4 + g, 0)};
+            lds_read_frags<2, 2>(qad, qf[0]);
+            reset_state();
+            tile_compute(0, ks, vs);
+            store_out();
+        };
+        for (uint32_t cur = bh;;) {
+            head_step(cur, k0, v0, qt0, k1, v1, qt1);
+            if ((cur += gridDim.x) >= a.nbh) break;
+            head_step(cur, k1, v1, qt1, k0, v0, qt0);
+            if ((cur += gridDim.x) >= a.nbh) break;
         }
     }
 }
@@ -545,16 +684,25 @@ int mbrt_attention_ex(const void* q, const void* k, const void* v, int dtype, in
     const int qs = n_q > kQBlock * MBRT_ATTN_QS2_MIN ? 2 : 1;
     a.qtiles = (uint32_t)ceil_div(n_q, (int64_t)kQBlock * qs);
     MBRT_REQUIRE(BH * a.qtiles < (int64_t(1) << 31), MBRT_E_SHAPE, "%s: too many tiles", op);
-    const dim3 grid((unsigned)(BH * a.qtiles));
+    a.nbh = (uint32_t)BH;
+    // heads of at most one query tile and one key tile, without the rotary or gate fusions:
+    // persistent workgroups that walk the heads (MBRT_ATTN_HEADS_WPC per CU)
+    const bool heads = MBRT_ATTN_HEADS_WPC > 0 && n_q <= kQBlock && n_k <= kKeys && rot_cos == nullptr &&
+                       gate == nullptr;
+    const dim3 grid(heads ? (unsigned)std::min<int64_t>(BH, (int64_t)cu_count() * std::max(MBRT_ATTN_HEADS_WPC, 1))
+                          : (unsigned)(BH * a.qtiles));
     hipStream_t stm = as_stream(stream);
     auto launch = [&](auto pm) {
         constexpr int PM = decltype(pm)::value;
-        if (qs == 2) {
-            if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 2, PM>), grid, dim3(kWaves * 64), 0, stm, a);
-            else hipLaunchKernelGGL((attention_kernel<F32, 2, PM>), grid, dim3(kWaves * 64), 0, stm, a);
+        if (heads) {
+            if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 1, PM, true>), grid, dim3(kWaves * 64), 0, stm, a);
+            else hipLaunchKernelGGL((attention_kernel<F32, 1, PM, true>), grid, dim3(kWaves * 64), 0, stm, a);
+        } else if (qs == 2) {
+            if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 2, PM, false>), grid, dim3(kWaves * 64), 0, stm, a);
+            else hipLaunchKernelGGL((attention_kernel<F32, 2, PM, false>), grid, dim3(kWaves * 64), 0, stm, a);
         } else {
-            if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 1, PM>), grid, dim3(kWaves * 64), 0, stm, a);
-            else hipLaunchKernelGGL((attention_kernel<F32, 1, PM>), grid, dim3(kWaves * 64), 0, stm, a);
+            if (out_dtype == BF16) hipLaunchKernelGGL((attention_kernel<BF16, 1, PM, false>), grid, dim3(kWaves * 64), 0, stm, a);
+            else hipLaunchKernelGGL((attention_kernel<F32, 1, PM, false>), grid, dim3(kWaves * 64), 0, stm, a);
         }
     };
     if (p_precision == MBRT_ATTN_P_BF16) launch(std::integral_constant<int, MBRT_ATTN_P_BF16>{});

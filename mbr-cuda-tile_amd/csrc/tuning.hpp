@@ -88,6 +88,9 @@
 #ifndef MBRT_SM_SHORT_RPG
 #define MBRT_SM_SHORT_RPG 2  // rows per lane group in those blocks
 #endif
+#ifndef MBRT_ATTN_HEADS_WPC
+#define MBRT_ATTN_HEADS_WPC 3  // attention over <= 64 queries and keys: persistent workgroups per CU, each walking heads (0: one head per workgroup)
+#endif
 #ifndef MBRT_ACT_U
 #define MBRT_ACT_U 2     // 16-byte groups per thread: bias + activation (GELU)
 #endif
