@@ -33,8 +33,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kTT = 64;   // frames per tile
 constexpr int kTJ = 64;   // band-bins per gather tile
-constexpr int kTF = 32;   // freqs per merge tile
-constexpr int kME = 64;   // CSR entries staged per merge chunk
+constexpr int kTF = MBRT_BAND_MTF;   // freqs per merge tile
+constexpr int kME = MBRT_BAND_MME;   // CSR entries staged per merge chunk
+constexpr int kMW = MBRT_BAND_MNW;   // waves per merge block
+static_assert(kTF <= 64 && kTF % kMW == 0 && kME % 64 == 0 && kTT % kMW == 0, "merge tile shape");
 
 __device__ __forceinline__ int64_t load_index(const void* p, int i64, int64_t i) {
     return i64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
@@ -372,7 +374,7 @@ struct MergeArgs {
 // stft * sum by the count and rounds; an F32 output adds, in ascending entry order, each
 // entry's stft * mask / count rounded to bf16.
 template <int MDT, int ODT, bool I64, bool FB>
-__global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(64 * kMW) void band_merge_kernel(MergeArgs a) {
     __shared__ f32x2 ms[kME][kTT + 1];
     // one linear grid; neighbouring freq tiles (whose CSR runs split cache lines of the
     // mask rows) run on one XCD
@@ -396,17 +398,20 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     const void* mask = a.mask[bs - b * a.S];
     const int lane = threadIdx.x % 64;
     const int w = wave_id();
-    constexpr int kPer = kTF / (kThreads / 64);  // freqs per wave (8)
-    constexpr int kR = kTT / (kThreads / 64);    // staged frames per wave (16)
+    constexpr int kPer = kTF / kMW;   // freqs per wave
+    constexpr int kR = kTT / kMW;     // staged frames per wave
+    constexpr int kEL = kME / 64;     // staged entries per lane
     const int nf = min(kTF, a.F - f0);           // freqs in this tile
     const int t = t0 + lane;
     const int tq = min(t, a.T - 1);
 
-    // CSR offsets of the tile's freqs: lane l holds off[f0 + l] (l <= nf), broadcast by readlane
+    // CSR offsets of the tile's freqs: lane l holds off[f0 + l] (l < nf; lane nf and up
+    // off[f0 + nf]), broadcast by readlane; off_end = off[f0 + nf]
     const int off_lane = ld_idx<I64>(a.off, f0 + min(lane, nf));
+    const int off_end = kTF < 64 ? __builtin_amdgcn_readlane(off_lane, kTF < 64 ? nf : 0) : ld_idx<I64>(a.off, f0 + nf);
     // with no band-bins (J = 0) no entry is read, whatever the offsets hold
     const int e_begin = __builtin_amdgcn_readlane(off_lane, 0);
-    const int e_end = a.J > 0 ? __builtin_amdgcn_readlane(off_lane, nf) : e_begin;
+    const int e_end = a.J > 0 ? off_end : e_begin;
     float c = load1(a.cnt, a.cdt, f0 + min(lane, nf - 1));
     const float den_lane = c > 1.0e-8f ? c : 1.0e-8f;
     const float inv_lane = 1.0f / den_lane;
@@ -414,34 +419,43 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     float den[kPer];
 #pragma unroll
     for (int r = 0; r < kPer; ++r)
-        den[r] = FB ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, den_lane), w + 4 * r))
+        den[r] = FB ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, den_lane), w + kMW * r))
                     : 1.0f;
 
     const f32x2* srow = reinterpret_cast<const f32x2*>(a.stft) + ((int64_t)b * a.F + f0) * a.T + tq;
     f32x2 sv[kPer], acc[kPer];
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
-        sv[r] = gld<MBRT_NT_BAND>(srow + (int64_t)min(w + 4 * r, nf - 1) * a.T);
+        sv[r] = gld<MBRT_NT_BAND>(srow + (int64_t)min(w + kMW * r, nf - 1) * a.T);
         acc[r] = f32x2{0.0f, 0.0f};
     }
     const int64_t mbase = (int64_t)b * a.T;
     for (int c0 = e_begin; c0 < e_end; c0 += kME) {
         const int c1 = min(c0 + kME, e_end);
         // entry and band-bin clamped into ind[0, J) and [0, J): offsets past J read in bounds
-        const int ei = min(max(min(c0 + lane, c1 - 1), 0), a.J - 1);
-        const int j = min(max(ld_idx<I64>(a.ind, ei), 0), a.J - 1);
-        f32x2 mv[kR];
+        int j[kEL];
 #pragma unroll
-        for (int r = 0; r < kR; ++r)
-            mv[r] = load_complex<MDT>(mask, (mbase + min(t0 + w + 4 * r, a.T - 1)) * a.J + j);
+        for (int h = 0; h < kEL; ++h) {
+            const int ei = min(max(min(c0 + 64 * h + lane, c1 - 1), 0), a.J - 1);
+            j[h] = min(max(ld_idx<I64>(a.ind, ei), 0), a.J - 1);
+        }
+        f32x2 mv[kEL][kR];
 #pragma unroll
-        for (int r = 0; r < kR; ++r) ms[lane][w + 4 * r] = mv[r];
+        for (int h = 0; h < kEL; ++h)
+#pragma unroll
+            for (int r = 0; r < kR; ++r)
+                mv[h][r] = load_complex<MDT>(mask, (mbase + min(t0 + w + kMW * r, a.T - 1)) * a.J + j[h]);
+#pragma unroll
+        for (int h = 0; h < kEL; ++h)
+#pragma unroll
+            for (int r = 0; r < kR; ++r) ms[64 * h + lane][w + kMW * r] = mv[h][r];
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
-            const int fl = w + 4 * r;  // local freq (wave-uniform); entries [off[f], off[f+1])
+            const int fl = w + kMW * r;  // local freq (wave-uniform); entries [off[f], off[f+1])
             const int lo = max(__builtin_amdgcn_readlane(off_lane, fl), c0);
-            const int hi = fl < nf ? min(__builtin_amdgcn_readlane(off_lane, fl + 1), c1) : lo;
+            const int nxt = fl + 1 < 64 ? __builtin_amdgcn_readlane(off_lane, min(fl + 1, 63)) : off_end;
+            const int hi = fl < nf ? min(nxt, c1) : lo;
             for (int e = lo; e < hi; ++e) {
                 const f32x2 m = ms[e - c0][lane];
                 if constexpr (!FB) {
@@ -462,12 +476,12 @@ __global__ __launch_bounds__(kThreads) void band_merge_kernel(MergeArgs a) {
     float inv[kPer];
 #pragma unroll
     for (int r = 0; r < kPer; ++r)
-        inv[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_lane), w + 4 * r));
+        inv[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv_lane), w + kMW * r));
     if (t >= a.T) return;
     const int64_t bins = a.F / a.C.d;
 #pragma unroll
     for (int r = 0; r < kPer; ++r) {
-        const int fl = w + 4 * r;
+        const int fl = w + kMW * r;
         if (fl < nf) {
             uint32_t bin, ch;
             fdivmod((uint32_t)(f0 + fl), a.C, bin, ch);
@@ -609,16 +623,16 @@ int mbrt_band_mask_merge(const float* stft, const void* const* masks, int mask_d
             if constexpr (M == BF16 && O != F16) {
                 if (fb) {
                     if (index_dtype == I64)
-                        hipLaunchKernelGGL((band_merge_kernel<M, O, true, true>), grid, dim3(kThreads), 0, as_stream(stream), a);
+                        hipLaunchKernelGGL((band_merge_kernel<M, O, true, true>), grid, dim3(64 * kMW), 0, as_stream(stream), a);
                     else
-                        hipLaunchKernelGGL((band_merge_kernel<M, O, false, true>), grid, dim3(kThreads), 0, as_stream(stream), a);
+                        hipLaunchKernelGGL((band_merge_kernel<M, O, false, true>), grid, dim3(64 * kMW), 0, as_stream(stream), a);
                     return;
                 }
             }
             if (index_dtype == I64)
-                hipLaunchKernelGGL((band_merge_kernel<M, O, true, false>), grid, dim3(kThreads), 0, as_stream(stream), a);
+                hipLaunchKernelGGL((band_merge_kernel<M, O, true, false>), grid, dim3(64 * kMW), 0, as_stream(stream), a);
             else
-                hipLaunchKernelGGL((band_merge_kernel<M, O, false, false>), grid, dim3(kThreads), 0, as_stream(stream), a);
+                hipLaunchKernelGGL((band_merge_kernel<M, O, false, false>), grid, dim3(64 * kMW), 0, as_stream(stream), a);
         });
     });
     return check_launch(op);

@@ -64,6 +64,15 @@
 #ifndef MBRT_BAND_GBPC
 #define MBRT_BAND_GBPC 1  // pipelined band gather: persistent blocks per CU
 #endif
+#ifndef MBRT_BAND_MTF
+#define MBRT_BAND_MTF 32  // band merge: freqs per tile (<= 64)
+#endif
+#ifndef MBRT_BAND_MME
+#define MBRT_BAND_MME 64  // band merge: CSR entries staged per chunk (a multiple of 64)
+#endif
+#ifndef MBRT_BAND_MNW
+#define MBRT_BAND_MNW 4  // band merge: waves per block
+#endif
 #ifndef MBRT_BAND_MERGE_TFAST
 #define MBRT_BAND_MERGE_TFAST 0  // band merge tile order: frame tiles fastest (1) or freq tiles fastest (0)
 #endif
