@@ -558,28 +558,23 @@ def main():
             mfma = op.flops / op.bytes > MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
             next_ops[op.name] = {"flops": op.flops, "bytes": op.bytes, "ms": round(ms, 5), "tflops": round(tf, 1),
                                  "frac_mfma_bf16_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                                 "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                                 "flop_per_byte": round(op.flops / op.bytes, 1), "bound": "mfma" if mfma else "hbm",
-                                 "kernel": op.kernel}
+                                 "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bound": "mfma" if mfma else "hbm"}
         else:
-            next_ops[op.name] = {"bytes": op.bytes, "ms": round(ms, 5), "gbs": round(gbs, 1),
-                                 "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "kernel": op.kernel}
+            next_ops[op.name] = {"bytes": op.bytes, "ms": round(ms, 5), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
         with_traffic(next_ops[op.name], op)
+        next_ops[op.name].pop("traffic", None)  # the ratio is kept; the line stays short
     ops = [o for o in ops if not o.next]
     for op in ops:
         ms = op.ms
         gbs = op.bytes / (ms * 1e-3) / 1e9
         per_op[op.name] = {"bytes": op.bytes, "ms": round(ms, 5),
-                           "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                           "dtype": op.name.rsplit("_", 1)[-1], "compute": "f32",
-                           "buffer_sets": len(op.sets), "kernel": op.kernel}
+                           "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "kernel": op.kernel}
         if op.copy_ms:
-            per_op[op.name]["copy_same_bytes_gbs"] = round(op.bytes / (op.copy_ms * 1e-3) / 1e9, 1)
             per_op[op.name]["frac_of_same_size_copy"] = round(op.copy_ms / ms, 4)
         if op.mix_ms:
-            per_op[op.name]["read1_write2_same_bytes_gbs"] = round(op.bytes / (op.mix_ms * 1e-3) / 1e9, 1)
             per_op[op.name]["frac_of_same_mix_kernel"] = round(op.mix_ms / ms, 4)
         with_traffic(per_op[op.name], op)
+        per_op[op.name].pop("traffic", None)
         if op.retimed:
             per_op[op.name]["retimed"] = op.retimed
         if gbs > HBM_PEAK_GBS:  # inputs are cycled past the MALL: this can only be a measurement error
@@ -619,14 +614,15 @@ def main():
             "workload": "mbr_chunk_tensor_ops: BL-1..BL-5 at full MelBandRoformer chunk shape "
                         "(T=801 frames, 60 bands, D=384, batch 4 band split), one pass per step",
             "ms_tensor_ops_per_step": round(tot_ms, 4),
-            "ms_per_step_note": "GPU time of one pass over all ops (sum of per-op means, each one "
-                                "HIP event pair over the op's K back-to-back calls); the timed "
-                                "region's wall clock, which also holds the stream holds and "
-                                "synchronisations, is wall_ms_per_step",
+            "ms_per_step_note": "sum of per-op means, each one HIP event pair over the op's K "
+                                "back-to-back calls; wall_ms_per_step adds the holds and syncs",
             "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
             "frac_hbm_peak_all_ops": round(value / HBM_PEAK_GBS, 4),
             "storage_dtypes": "f32 and bf16 per op name; all arithmetic in f32",
             "mall_defeat": f"each op cycles >= {MALL_DEFEAT_BYTES / 1e9:.1f} GB of buffer sets",
+            "per_op_fields": "traffic_over_algorithmic: rocprofv3 FETCH_SIZE + WRITE_SIZE per launch "
+                             "(profiles/traffic_all_ops.md) over bytes; frac_of_same_size_copy: a plain "
+                             "copy of the same bytes timed beside the op, over the op's time",
             "per_op": per_op,
             "next_ops": next_ops,
         },
@@ -643,8 +639,13 @@ def main():
             "avg_ms": round(dom_ms, 5),
         },
         "cpu_baseline": None if args.no_cpu else cpu_baseline(args.cpu_threads),
+        # the same fractions in two short maps, last on the line: BL ops of the HBM peak, the
+        # widened ops of the roof that bounds each (bf16 MFMA or HBM)
+        "frac_hbm_peak_per_op": {k: v["frac_hbm_peak"] for k, v in per_op.items()},
+        "frac_of_roof_next_ops": {k: v["frac_mfma_bf16_peak" if v.get("bound") == "mfma" else "frac_hbm_peak"]
+                                  for k, v in next_ops.items()},
     }
-    print(json.dumps(line), flush=True)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":
