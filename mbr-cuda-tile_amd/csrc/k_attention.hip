@@ -173,6 +173,28 @@ __device__ __forceinline__ void lds_read_frags(const uint32_t (&ad)[NA], bf16x8 
     for (int i = 0; i < N; ++i) f[i] = __builtin_bit_cast(bf16x8, r[i]);
 }
 
+// LDS writes and reads of the persistent form's output staging, as asm so that the
+// compiler, which cannot tell this wave's staging rows from the next head's tiles loading
+// into other buffers, does not wait for those loads (vmcnt 0) before them.  The writes
+// end with their own lgkmcnt(0); the two reads of lds_read_b128_x2 complete before it
+// returns.
+__device__ __forceinline__ void lds_write_b64(uint32_t ad, u32x2 v) {
+    asm volatile("ds_write_b64 %0, %1" ::"v"(ad), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_write_b128(uint32_t ad, u32x4 v) {
+    asm volatile("ds_write_b128 %0, %1" ::"v"(ad), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void lds_read_b128_x2(uint32_t a0, uint32_t a1, u32x4& r0, u32x4& r1) {
+    asm volatile(
+        "ds_read_b128 %0, %2\n\t"
+        "ds_read_b128 %1, %3\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r0), "=&v"(r1)
+        : "v"(a0), "v"(a1)
+        : "memory");
+}
+
 __device__ __forceinline__ float xor_sum(float x) {
     x += __shfl_xor(x, 16);
     return x + __shfl_xor(x, 32);
@@ -343,9 +365,9 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(HEA
             const uint32_t chunk = 8 * ((lane & 7) ^ (lane >> 3));
             const uint32_t koff = (uint32_t)min(row, a.nk - 1) * a.kv_rs + chunk;
             const uint32_t qoff = (uint32_t)min(row, a.nq - 1) * a.q_rs + chunk;
-            __builtin_amdgcn_global_load_lds((global_void*)(kb + koff), (lds_void*)&kd[r0 * kHeadDim], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((global_void*)(vb + koff), (lds_void*)&vd[r0 * kHeadDim], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((global_void*)(qb + qoff), (lds_void*)&qd[r0 * kHeadDim], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(kb + koff), (lds_void*)&kd[r0 * kHeadDim], 16, 0, (MBRT_ATTN_HEADS_NT & 2) ? kCpolNt : 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(vb + koff), (lds_void*)&vd[r0 * kHeadDim], 16, 0, (MBRT_ATTN_HEADS_NT & 2) ? kCpolNt : 0);
+            __builtin_amdgcn_global_load_lds((global_void*)(qb + qoff), (lds_void*)&qd[r0 * kHeadDim], 16, 0, (MBRT_ATTN_HEADS_NT & 2) ? kCpolNt : 0);
         }
     };
     if constexpr (HEADS) load_head(bh, k0, v0, qt0);
@@ -578,7 +600,56 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(HEA
         // exactly its kStores output stores behind the loads of `cur`, waiting until at most
         // kStores are outstanding completes those loads and leaves the stores in flight.
         // A wave without queries (q0 >= n_q) stores nothing and waits for all.
-        constexpr int kStores = 4;  // output stores per wave and head: one per 16-wide d block
+        // The output leaves through this wave's 16 rows of the head's Q tile (2 KB, free once
+        // the Q fragments are in registers, private to the wave): O is written there in
+        // query rows, each 16-byte chunk at chunk ^ (row % 8), and read back as whole rows,
+        // so every store instruction writes 8 full query rows (1 KB of a bf16 output, 512 B
+        // per half of an f32 one) instead of 32 bytes in each of 16 rows.  Rows past n_q
+        // were computed from the clamped query row n_q - 1 and hold its output bit for bit;
+        // they are stored again over row n_q - 1, so every store instruction has all lanes
+        // active and the store count per head is fixed.
+        constexpr int kStores = ODT == F32 ? 4 : 2;  // output stores per wave and head
+        auto store_staged = [&](const __bf16* qs) {
+            const float lsum = kSumMfma ? osum[0][0] : xor_sum(l[0]);
+            const float inv = 1.0f / lsum;
+            const uint32_t base = lds_addr(qs) + 16u * 128u * (uint32_t)w;
+            const int r0 = lane >> 3, r1 = 8 + (lane >> 3), ck = lane & 7;
+            const uint32_t rd0 = base + 128u * r0 + 16u * (uint32_t)(ck ^ (r0 & 7));
+            const uint32_t rd1 = base + 128u * r1 + 16u * (uint32_t)(ck ^ (r1 & 7));
+            const int64_t row0 = (int64_t)bh * a.nq + min(q0 + r0, a.nq - 1);
+            const int64_t row1 = (int64_t)bh * a.nq + min(q0 + r1, a.nq - 1);
+            if constexpr (ODT == F32) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                    for (int k2 = 0; k2 < 2; ++k2) {
+                        const f32x4 v = o[0][2 * hh + k2] * inv;
+                        lds_write_b128(base + 128u * c + 16u * (uint32_t)((4 * k2 + g) ^ (c & 7)),
+                                       __builtin_bit_cast(u32x4, v));
+                    }
+                    lds_wait();
+                    u32x4 v0, v1;
+                    lds_read_b128_x2(rd0, rd1, v0, v1);
+                    float* out = reinterpret_cast<float*>(a.out);
+                    gst<(MBRT_ATTN_HEADS_NT & 1) ? 2 : 0>(reinterpret_cast<u32x4*>(out + row0 * kHeadDim + 32 * hh + 4 * ck), v0);
+                    gst<(MBRT_ATTN_HEADS_NT & 1) ? 2 : 0>(reinterpret_cast<u32x4*>(out + row1 * kHeadDim + 32 * hh + 4 * ck), v1);
+                }
+            } else {
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    u32x2 pk;
+                    pk.x = pack_bf16x2(o[0][db][0] * inv, o[0][db][1] * inv);
+                    pk.y = pack_bf16x2(o[0][db][2] * inv, o[0][db][3] * inv);
+                    lds_write_b64(base + 128u * c + 16u * (uint32_t)((2 * db + (g >> 1)) ^ (c & 7)) + 8u * (g & 1), pk);
+                }
+                lds_wait();
+                u32x4 v0, v1;
+                lds_read_b128_x2(rd0, rd1, v0, v1);
+                uint16_t* out = reinterpret_cast<uint16_t*>(a.out);
+                gst<(MBRT_ATTN_HEADS_NT & 1) ? 2 : 0>(reinterpret_cast<u32x4*>(out + row0 * kHeadDim + 8 * ck), v0);
+                gst<(MBRT_ATTN_HEADS_NT & 1) ? 2 : 0>(reinterpret_cast<u32x4*>(out + row1 * kHeadDim + 8 * ck), v1);
+            }
+        };
         bool first = true;
         auto head_step = [&](uint32_t cur, const __bf16* ks, const __bf16* vs, const __bf16* qs, __bf16* kn,
                              __bf16* vn, __bf16* qn) {
@@ -597,7 +668,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(HEA
             lds_read_frags<2, 2>(qad, qf[0]);
             reset_state();
             tile_compute(0, ks, vs);
-            store_out();
+            store_staged(qs);
         };
         for (uint32_t cur = bh;;) {
             head_step(cur, k0, v0, qt0, k1, v1, qt1);

@@ -19,6 +19,18 @@
 namespace mbrt {
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// float4 through the non-temporal load / store helpers (which take ext-vector types)
+template <int NT>
+__device__ __forceinline__ float4 ld4(const float4* p) {
+    const f32x4 v = gld<NT>(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <int NT>
+__device__ __forceinline__ void st4(float4* p, float4 v) {
+    gst<NT>(reinterpret_cast<f32x4*>(p), f32x4{v.x, v.y, v.z, v.w});
+}
+
 constexpr int kThreads = 256;
 
 struct AccArgs {
@@ -94,14 +106,14 @@ __global__ __launch_bounds__(64 * CPB) void accumulate_cw_kernel(AccArgs a) {
     for (int64_t k = (int64_t)blockIdx.x * 64 + lane; k < a.n; k += (int64_t)gridDim.x * 64) {
         const float4 wv = reinterpret_cast<const float4*>(a.win)[k];
         if (c < a.channels) {
-            const float4 s = reinterpret_cast<const float4*>(a.src)[c * a.n + k];
+            const float4 s = ld4<MBRT_NT_CHUNK & 1>(reinterpret_cast<const float4*>(a.src) + c * a.n + k);
             float4* dp = reinterpret_cast<float4*>(a.dest) + c * a.dest_len + a.offset + k;
-            float4 d = *dp;
+            float4 d = ld4<MBRT_NT_CHUNK & 1>(dp);
             d.x = acc1(d.x, s.x, wv.x);
             d.y = acc1(d.y, s.y, wv.y);
             d.z = acc1(d.z, s.z, wv.z);
             d.w = acc1(d.w, s.w, wv.w);
-            *dp = d;
+            st4<MBRT_NT_CHUNK & 2>(dp, d);
         }
         if (blockIdx.y == 0 && w == 0) {
             float4* wp = reinterpret_cast<float4*>(a.wsum) + a.offset + k;
@@ -137,12 +149,12 @@ __global__ __launch_bounds__(kThreads) void normalize_vec_kernel(NormArgs a) {
 #pragma unroll 4
         for (int64_t c = 0; c < a.channels; ++c) {
             float4* p = reinterpret_cast<float4*>(a.data) + c * a.len + k;
-            float4 v = *p;
+            float4 v = ld4<MBRT_NT_CHUNK & 1>(p);
             v.x = norm1(v.x, w.x);
             v.y = norm1(v.y, w.y);
             v.z = norm1(v.z, w.z);
             v.w = norm1(v.w, w.w);
-            *p = v;
+            st4<MBRT_NT_CHUNK & 2>(p, v);
         }
     }
 }

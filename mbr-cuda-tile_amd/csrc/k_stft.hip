@@ -540,7 +540,7 @@ __global__ __launch_bounds__(64 * TF) void stft_kernel(StftArgs a) {
 #pragma unroll 4
     for (int f = fr; f < kBins; f += NT / TF, dst += step) {
         const float2 X = src[pad16(f)];
-        *dst = make_float2(X.x * a.norm, X.y * a.norm);
+        gst<MBRT_NT_STFT & 2>(reinterpret_cast<f32x2*>(dst), f32x2{X.x * a.norm, X.y * a.norm});
     }
 }
 
@@ -567,9 +567,10 @@ struct IstftBlockArgs {
 template <int SDT>
 __device__ __forceinline__ float2 load_bin(const void* spec, int64_t i) {
     if constexpr (SDT == F32) {
-        return static_cast<const float2*>(spec)[i];
+        const f32x2 v = gld<MBRT_NT_STFT & 1>(static_cast<const f32x2*>(spec) + i);
+        return make_float2(v.x, v.y);
     } else {
-        const uint32_t u = static_cast<const uint32_t*>(spec)[i];
+        const uint32_t u = gld<MBRT_NT_STFT & 1>(static_cast<const uint32_t*>(spec) + i);
         return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
     }
 }
@@ -659,7 +660,7 @@ __global__ __launch_bounds__(64 * TF) void istft_block_kernel(IstftBlockArgs a) 
         const uint32_t jlo = u >= (uint32_t)kN ? fdiv(u - kN, a.hop) + 1 : 0;
         float acc = 0.0f;
         for (uint32_t j = jlo; j <= jhi; ++j) acc += reinterpret_cast<const float*>(lds + j * kSlot)[u - j * hop];
-        part[u] = acc;
+        gst<MBRT_NT_ISTFT & 2>(part + u, acc);
     }
 }
 
@@ -684,7 +685,7 @@ __global__ __launch_bounds__(256) void istft_final_kernel(IstftFinalArgs a) {
     const uint32_t hop = a.hop.d, bhop = a.bhop.d;
     for (uint32_t so = blockIdx.x * 256 + threadIdx.x; so < a.out_len; so += gridDim.x * 256) {
         if (so >= a.valid) {
-            for (uint32_t b = 0; b < a.batch; ++b) a.out[(int64_t)b * a.out_len + so] = 0.0f;
+            for (uint32_t b = 0; b < a.batch; ++b) gst<(MBRT_NT_ISTFT & 4) ? 2 : 0>(a.out + (int64_t)b * a.out_len + so, 0.0f);
             continue;
         }
         const uint32_t s = so + a.offset;
@@ -723,8 +724,8 @@ __global__ __launch_bounds__(256) void istft_final_kernel(IstftFinalArgs a) {
 #pragma unroll
                 for (uint32_t k = 0; k < 4; ++k) {
                     const float* pb = a.part + (int64_t)min(b0 + k, a.batch - 1) * a.ntb * a.span;
-                    p[k][0] = pb[off[0]];
-                    p[k][1] = pb[off[1]];
+                    p[k][0] = gld<MBRT_NT_ISTFT & 1>(pb + off[0]);
+                    p[k][1] = gld<MBRT_NT_ISTFT & 1>(pb + off[1]);
                 }
 #pragma unroll
                 for (uint32_t k = 0; k < 4; ++k) {
@@ -732,7 +733,7 @@ __global__ __launch_bounds__(256) void istft_final_kernel(IstftFinalArgs a) {
                     float acc = 0.0f;
                     if (v[0]) acc += p[k][0];
                     if (v[1]) acc += p[k][1];
-                    a.out[(int64_t)(b0 + k) * a.out_len + so] = ws > 1.0e-8f ? acc / ws : acc;
+                    gst<(MBRT_NT_ISTFT & 4) ? 2 : 0>(a.out + (int64_t)(b0 + k) * a.out_len + so, ws > 1.0e-8f ? acc / ws : acc);
                 }
             }
             continue;
@@ -744,9 +745,9 @@ __global__ __launch_bounds__(256) void istft_final_kernel(IstftFinalArgs a) {
             for (uint32_t tb = blo; tb <= bhi; ++tb) {
                 const uint32_t u = s - tb * bhop;
                 const uint32_t nf = min((uint32_t)kTF, a.T - tb * kTF);
-                if (u < (nf - 1) * hop + kN) acc += pb[(int64_t)tb * a.span + u];
+                if (u < (nf - 1) * hop + kN) acc += gld<MBRT_NT_ISTFT & 1>(pb + (int64_t)tb * a.span + u);
             }
-            a.out[(int64_t)b * a.out_len + so] = ws > 1.0e-8f ? acc / ws : acc;
+            gst<(MBRT_NT_ISTFT & 4) ? 2 : 0>(a.out + (int64_t)b * a.out_len + so, ws > 1.0e-8f ? acc / ws : acc);
         }
     }
 }

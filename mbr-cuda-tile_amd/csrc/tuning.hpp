@@ -42,6 +42,15 @@
 #ifndef MBRT_NT_EW
 #define MBRT_NT_EW 0     // convert / unary / scalar / binary vector kernels
 #endif
+#ifndef MBRT_NT_STFT
+#define MBRT_NT_STFT 0   // STFT spectrum stores (bit 1), iSTFT spectrum loads (bit 0)
+#endif
+#ifndef MBRT_NT_ISTFT
+#define MBRT_NT_ISTFT 4  // iSTFT block partials: final-pass loads (bit 0), block stores (bit 1); output stores (bit 2)
+#endif
+#ifndef MBRT_NT_CHUNK
+#define MBRT_NT_CHUNK 3  // chunk accumulate and normalize: chunk and output loads (bit 0), output stores (bit 1)
+#endif
 #ifndef MBRT_NT_BAND
 #define MBRT_NT_BAND 2   // band gather / mask merge: stft, masks, outputs
 #endif
@@ -99,6 +108,9 @@
 #endif
 #ifndef MBRT_ATTN_HEADS_WPC
 #define MBRT_ATTN_HEADS_WPC 3  // attention over <= 64 queries and keys: persistent workgroups per CU, each walking heads (0: one head per workgroup)
+#endif
+#ifndef MBRT_ATTN_HEADS_NT
+#define MBRT_ATTN_HEADS_NT 3  // persistent attention over short heads: non-temporal output stores (bit 0) and K/V/Q loads (bit 1)
 #endif
 #ifndef MBRT_ACT_U
 #define MBRT_ACT_U 2     // 16-byte groups per thread: bias + activation (GELU)
