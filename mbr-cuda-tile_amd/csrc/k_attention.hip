@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(HEA
     for (int x = 0; x < QS; ++x) {
         const __bf16* qrow = a.q + b * a.q_bs + h * a.q_hs + (int64_t)min(q0 + 16 * x + c, a.nq - 1) * a.q_rs;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) qf[x][s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g);
+        for (int s = 0; s < 2; ++s) qf[x][s] = gld<MBRT_ATTN_NT & 1>(reinterpret_cast<const bf16x8*>(qrow + 32 * s + 8 * g));
     }
     }
     if (!HEADS && a.cosp != nullptr) {
@@ -560,14 +560,14 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(HEA
             for (int db = 0; db < 4; ++db) {
                 const int64_t e = tok * kHeadDim + 16 * db + 4 * g;
                 if constexpr (ODT == F32) {
-                    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + e) = (o[x][db] * inv) * gv;
+                    gst<MBRT_ATTN_NT & 2>(reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + e), (o[x][db] * inv) * gv);
                 } else {
                     const uint32_t r0 = pack_bf16x2(o[x][db][0] * inv, o[x][db][1] * inv);
                     const uint32_t r1 = pack_bf16x2(o[x][db][2] * inv, o[x][db][3] * inv);
                     u32x2 pk;
                     pk.x = pack_bf16x2(bf16_lo(r0) * gv, bf16_hi(r0) * gv);
                     pk.y = pack_bf16x2(bf16_lo(r1) * gv, bf16_hi(r1) * gv);
-                    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + e) = pk;
+                    gst<MBRT_ATTN_NT & 2>(reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + e), pk);
                 }
             }
             continue;
@@ -577,12 +577,12 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(HEA
         for (int db = 0; db < 4; ++db) {
             const int d = 16 * db + 4 * g;
             if constexpr (ODT == F32) {
-                *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + obase + d) = o[x][db] * inv;
+                gst<MBRT_ATTN_NT & 2>(reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + obase + d), o[x][db] * inv);
             } else {
                 u32x2 pk;
                 pk.x = pack_bf16x2(o[x][db][0] * inv, o[x][db][1] * inv);
                 pk.y = pack_bf16x2(o[x][db][2] * inv, o[x][db][3] * inv);
-                *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + obase + d) = pk;
+                gst<MBRT_ATTN_NT & 2>(reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.out) + obase + d), pk);
             }
         }
     }

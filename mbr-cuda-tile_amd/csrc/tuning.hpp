@@ -109,6 +109,9 @@
 #ifndef MBRT_ATTN_HEADS_WPC
 #define MBRT_ATTN_HEADS_WPC 3  // attention over <= 64 queries and keys: persistent workgroups per CU, each walking heads (0: one head per workgroup)
 #endif
+#ifndef MBRT_ATTN_NT
+#define MBRT_ATTN_NT 0  // attention, one workgroup per query tile: non-temporal q loads (bit 0) and output stores (bit 1); measured: no gain
+#endif
 #ifndef MBRT_ATTN_HEADS_NT
 #define MBRT_ATTN_HEADS_NT 3  // persistent attention over short heads: non-temporal output stores (bit 0) and K/V/Q loads (bit 1)
 #endif
