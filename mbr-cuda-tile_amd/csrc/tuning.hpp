@@ -107,7 +107,7 @@
 #define MBRT_SM_SHORT_RPG 2  // rows per lane group in those blocks
 #endif
 #ifndef MBRT_ATTN_HEADS_WPC
-#define MBRT_ATTN_HEADS_WPC 3  // attention over <= 64 queries and keys: persistent workgroups per CU, each walking heads (0: one head per workgroup)
+#define MBRT_ATTN_HEADS_WPC 2  // attention over <= 64 queries and keys: persistent workgroups per CU, each walking heads (0: one head per workgroup)
 #endif
 #ifndef MBRT_ATTN_NT
 #define MBRT_ATTN_NT 0  // attention, one workgroup per query tile: non-temporal q loads (bit 0) and output stores (bit 1); measured: no gain

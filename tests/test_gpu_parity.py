@@ -856,7 +856,7 @@ def test_attention_p_bf16_fast(orc, dev, BH, nq, nk, odt):
                                                  fast=True))
 
 
-# Heads of at most 64 queries and 64 keys run on persistent workgroups (3 per CU), each
+# Heads of at most 64 queries and 64 keys run on persistent workgroups, each
 # walking heads with the next head's K, V and Q loading while it computes: more heads than
 # workgroups, waves without queries (n_q <= 48), one query, one key, every P precision.
 @pytest.mark.parametrize("BH,nq,nk", [(2000, 60, 60), (1601, 17, 64), (1000, 64, 5), (900, 1, 33), (777, 33, 1)])
