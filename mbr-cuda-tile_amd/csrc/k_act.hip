@@ -173,6 +173,7 @@ struct GateArgs {
     FastDiv gpt;       // groups per token = H*D/VE
     FastDiv gph;       // groups per head = D/VE
     FastDiv n_div;     // N
+    FastDiv h_div;     // H
     int fb;            // bf16 intermediates (element kernel; the vector kernel takes FB)
 };
 
@@ -185,19 +186,32 @@ __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
     const int64_t base = chunk * (kThreads * kUGate) + threadIdx.x;
     Vec<ADT, VE> av[kUGate];
     float gl[kUGate];
+    int64_t dst[kUGate];
 #pragma unroll
     for (int u = 0; u < kUGate; ++u) {
         const uint32_t g = (uint32_t)clamp_group(base + u * kThreads, a.groups);
         uint32_t token, rem, h, c;
-        fdivmod(g, a.gpt, token, rem);
-        fdivmod(rem, a.gph, h, c);
         int64_t src;
-        if (a.layout == MBRT_LAYOUT_BHND) {
-            uint32_t b, n;
-            fdivmod(token, a.n_div, b, n);
-            src = (((int64_t)b * a.H + h) * a.N + n) * a.D + (int64_t)c * VE;
-        } else {
+        if (MBRT_GATE_INORDER && a.layout == MBRT_LAYOUT_BHND) {
+            // g counts groups in the input's order: c fastest, then n, h, b
+            uint32_t r1, r2, n, b;
+            fdivmod(g, a.gph, r1, c);
+            fdivmod(r1, a.n_div, r2, n);
+            fdivmod(r2, a.h_div, b, h);
+            token = b * (uint32_t)a.N + n;
             src = (int64_t)g * VE;
+            dst[u] = (((int64_t)token * a.H + h) * a.gph.d + c) * VE;
+        } else {
+            fdivmod(g, a.gpt, token, rem);
+            fdivmod(rem, a.gph, h, c);
+            if (a.layout == MBRT_LAYOUT_BHND) {
+                uint32_t b, n;
+                fdivmod(token, a.n_div, b, n);
+                src = (((int64_t)b * a.H + h) * a.N + n) * a.D + (int64_t)c * VE;
+            } else {
+                src = (int64_t)g * VE;
+            }
+            dst[u] = (int64_t)g * VE;
         }
         av[u].template load<MBRT_NT_GATE>(a.attn, src);
         gl[u] = ld1<GDT>(a.gate, (int64_t)token * a.H + h);
@@ -214,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
             for (int i = 0; i < VE; ++i) v[i] = FB ? bf16r(v[i] * gv) : v[i] * gv;
             Vec<ODT, VE> o;
             o.from_f32(v);
-            o.template store<MBRT_NT_GATE>(a.out, g * VE);
+            o.template store<MBRT_NT_GATE>(a.out, dst[u]);
         }
     }
     }
@@ -374,6 +388,7 @@ int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const void* gate, 
         a.gpt = make_fastdiv((uint32_t)(H * D / ve));
         a.gph = make_fastdiv((uint32_t)(D / ve));
         a.n_div = make_fastdiv((uint32_t)N);
+        a.h_div = make_fastdiv((uint32_t)H);
         with_dt(attn_dtype, [&](auto at) {
             with_dt(gate_dtype, [&](auto gt) {
                 with_dt(out_dtype, [&](auto ot) {

@@ -115,6 +115,9 @@
 #ifndef MBRT_ATTN_HEADS_NT
 #define MBRT_ATTN_HEADS_NT 3  // persistent attention over short heads: non-temporal output stores (bit 0) and K/V/Q loads (bit 1)
 #endif
+#ifndef MBRT_GATE_INORDER
+#define MBRT_GATE_INORDER 0  // gate merge of a head-major [B,H,N,D] input: threads in input order (1) or output order (0)
+#endif
 #ifndef MBRT_ACT_U
 #define MBRT_ACT_U 2     // 16-byte groups per thread: bias + activation (GELU)
 #endif
