@@ -30,8 +30,12 @@ __device__ __forceinline__ int64_t clamp_group(int64_t g, int64_t groups) { retu
 __device__ __forceinline__ int64_t ceil_div_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // GELU rounded to bf16/f16 uses the A&S 7.1.26 complement; f32 output uses erfcf.
-template <bool LOWP>
+// ACT >= 0 fixes the activation at compile time (the element loop is then straight-line
+// code); ACT < 0 takes it from `act` at run time.
+template <bool LOWP, int ACT = -1>
 __device__ __forceinline__ float act_fn(float v, int act) {
+    if constexpr (ACT == MBRT_ACT_GELU_REF) return LOWP ? gelu_ref_lowp(v) : gelu_ref(v);
+    if constexpr (ACT == MBRT_ACT_GELU_STD) return LOWP ? gelu_std_lowp(v) : gelu_std(v);
     switch (act) {
         case MBRT_ACT_GELU_REF: return LOWP ? gelu_ref_lowp(v) : gelu_ref(v);
         case MBRT_ACT_GELU_STD: return LOWP ? gelu_std_lowp(v) : gelu_std(v);
@@ -54,7 +58,7 @@ struct BiasActArgs {
     FastDiv cols_div;  // cols (vector path with bias needs cols % VE == 0 and n < 2^32)
 };
 
-template <int XDT, int ODT, int BDT>
+template <int XDT, int ODT, int BDT, int ACT>
 __global__ __launch_bounds__(kThreads) void bias_act_vec_kernel(BiasActArgs a) {
     constexpr int VE = (XDT == F32 || ODT == F32 || BDT == F32) ? 4 : 8;
     constexpr bool LOWP = ODT != F32;
@@ -85,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void bias_act_vec_kernel(BiasActArgs a) {
                     for (int i = 0; i < VE; ++i) v[i] += b[i];
                 }
 #pragma unroll
-                for (int i = 0; i < VE; ++i) v[i] = act_fn<LOWP>(v[i], a.act);
+                for (int i = 0; i < VE; ++i) v[i] = act_fn<LOWP, ACT>(v[i], a.act);
                 Vec<ODT, VE> o;
                 o.from_f32(v);
                 o.template store<MBRT_NT_ACT>(a.out, g * VE);
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(kThreads) void bias_act_vec_kernel(BiasActArgs a) {
     }
     if (blockIdx.x == 0) {  // tail when n % VE != 0 (only possible without bias)
         const int64_t e = groups * VE + threadIdx.x;
-        if (e < a.n) st1<ODT>(a.out, e, act_fn<LOWP>(ld1<XDT>(a.x, e), a.act));
+        if (e < a.n) st1<ODT>(a.out, e, act_fn<LOWP, ACT>(ld1<XDT>(a.x, e), a.act));
     }
 }
 
@@ -298,14 +302,24 @@ int mbrt_bias_act(const void* x, int x_dtype, const void* bias, int bias_dtype, 
     if (vec) {
         if (bias != nullptr) a.cols_div = make_fastdiv((uint32_t)cols);
         const dim3 grid = vec_grid(a.n / ve);
-        with_dt(x_dtype, [&](auto xt) {
-            with_dt(out_dtype, [&](auto ot) {
-                constexpr int X = decltype(xt)::value, O = decltype(ot)::value;
-                if (bias == nullptr) hipLaunchKernelGGL((bias_act_vec_kernel<X, O, kNoBias>), grid, dim3(kThreads), 0, st, a);
-                else if (bias_dtype == F32) hipLaunchKernelGGL((bias_act_vec_kernel<X, O, F32>), grid, dim3(kThreads), 0, st, a);
-                else hipLaunchKernelGGL((bias_act_vec_kernel<X, O, BF16>), grid, dim3(kThreads), 0, st, a);
+        // the two GELU forms (the model's activations) get kernels of their own
+        auto launch = [&](auto act_tag) {
+            constexpr int A = decltype(act_tag)::value;
+            with_dt(x_dtype, [&](auto xt) {
+                with_dt(out_dtype, [&](auto ot) {
+                    constexpr int X = decltype(xt)::value, O = decltype(ot)::value;
+                    if (bias == nullptr)
+                        hipLaunchKernelGGL((bias_act_vec_kernel<X, O, kNoBias, A>), grid, dim3(kThreads), 0, st, a);
+                    else if (bias_dtype == F32)
+                        hipLaunchKernelGGL((bias_act_vec_kernel<X, O, F32, A>), grid, dim3(kThreads), 0, st, a);
+                    else
+                        hipLaunchKernelGGL((bias_act_vec_kernel<X, O, BF16, A>), grid, dim3(kThreads), 0, st, a);
+                });
             });
-        });
+        };
+        if (act == MBRT_ACT_GELU_REF) launch(std::integral_constant<int, MBRT_ACT_GELU_REF>{});
+        else if (act == MBRT_ACT_GELU_STD) launch(std::integral_constant<int, MBRT_ACT_GELU_STD>{});
+        else launch(std::integral_constant<int, -1>{});
     } else {
         hipLaunchKernelGGL(bias_act_elem_kernel, elem_grid(a.n), dim3(kThreads), 0, st, a);
     }
