@@ -380,7 +380,23 @@ __global__ __launch_bounds__(64 * kMW) void band_merge_kernel(MergeArgs a) {
     // mask rows) run on one XCD
     const uint32_t tile = xcd_runs<MBRT_BAND_XCD>(blockIdx.x, a.tiles);
     uint32_t tf, tt, rest;
-    if constexpr (MBRT_BAND_MERGE_TFAST) {
+    if constexpr (MBRT_BAND_MERGE_PAIRS) {
+        // pairs of frame tiles: tiles (f, 2p) and (f, 2p + 1) are consecutive, then f + 1, so
+        // that a run of 8 tiles on one XCD holds 4 freq tiles x 2 frame tiles (an odd last
+        // frame tile follows the pairs, freq tiles in order)
+        const uint32_t per = a.tiles_f * a.tiles_t;
+        rest = tile / per;
+        const uint32_t sidx = tile - rest * per;
+        const uint32_t paired = (a.tiles_t / 2) * 2 * a.tiles_f;
+        if (sidx < paired) {
+            const uint32_t p = sidx / (2 * a.tiles_f), r = sidx - p * 2 * a.tiles_f;
+            tf = r / 2;
+            tt = 2 * p + (r & 1);
+        } else {
+            tt = a.tiles_t - 1;
+            tf = sidx - paired;
+        }
+    } else if constexpr (MBRT_BAND_MERGE_TFAST) {
         tt = tile % a.tiles_t;
         rest = tile / a.tiles_t;
         tf = rest % a.tiles_f;

@@ -82,6 +82,9 @@
 #ifndef MBRT_BAND_MNW
 #define MBRT_BAND_MNW 4  // band merge: waves per block
 #endif
+#ifndef MBRT_BAND_MERGE_PAIRS
+#define MBRT_BAND_MERGE_PAIRS 0  // band merge tile order: pairs of frame tiles within the freq-fastest order (1)
+#endif
 #ifndef MBRT_BAND_MERGE_TFAST
 #define MBRT_BAND_MERGE_TFAST 0  // band merge tile order: frame tiles fastest (1) or freq tiles fastest (0)
 #endif
