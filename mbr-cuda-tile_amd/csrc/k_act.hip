@@ -177,7 +177,8 @@ struct GateArgs {
     FastDiv gpt;       // groups per token = H*D/VE
     FastDiv gph;       // groups per head = D/VE
     FastDiv n_div;     // N
-    FastDiv h_div;     // H
+    FastDiv sb_div;    // MBRT_GATE_TPW * groups per token
+    int tpw_ok;        // B * N is a multiple of MBRT_GATE_TPW
     int fb;            // bf16 intermediates (element kernel; the vector kernel takes FB)
 };
 
@@ -196,14 +197,18 @@ __global__ __launch_bounds__(kThreads) void gate_merge_vec_kernel(GateArgs a) {
         const uint32_t g = (uint32_t)clamp_group(base + u * kThreads, a.groups);
         uint32_t token, rem, h, c;
         int64_t src;
-        if (MBRT_GATE_INORDER && a.layout == MBRT_LAYOUT_BHND) {
-            // g counts groups in the input's order: c fastest, then n, h, b
-            uint32_t r1, r2, n, b;
-            fdivmod(g, a.gph, r1, c);
-            fdivmod(r1, a.n_div, r2, n);
-            fdivmod(r2, a.h_div, b, h);
-            token = b * (uint32_t)a.N + n;
-            src = (int64_t)g * VE;
+        if (MBRT_GATE_TPW > 1 && a.tpw_ok && a.layout == MBRT_LAYOUT_BHND) {
+            // super-blocks of TPW tokens x all heads; within one, c fastest, then the token,
+            // then the head: a head's TPW rows are read as one run of TPW * D elements, and
+            // each token row is written in runs of (heads covered) * D
+            uint32_t sb, r, r2, ti, b, n;
+            fdivmod(g, a.sb_div, sb, r);
+            fdivmod(r, a.gph, r2, c);
+            h = r2 / MBRT_GATE_TPW;
+            ti = r2 - h * MBRT_GATE_TPW;
+            token = sb * MBRT_GATE_TPW + ti;
+            fdivmod(token, a.n_div, b, n);
+            src = (((int64_t)b * a.H + h) * a.N + n) * a.D + (int64_t)c * VE;
             dst[u] = (((int64_t)token * a.H + h) * a.gph.d + c) * VE;
         } else {
             fdivmod(g, a.gpt, token, rem);
@@ -402,7 +407,8 @@ int mbrt_sigmoid_gate_merge(const void* attn, int attn_dtype, const void* gate, 
         a.gpt = make_fastdiv((uint32_t)(H * D / ve));
         a.gph = make_fastdiv((uint32_t)(D / ve));
         a.n_div = make_fastdiv((uint32_t)N);
-        a.h_div = make_fastdiv((uint32_t)H);
+        a.sb_div = make_fastdiv((uint32_t)(MBRT_GATE_TPW * H * D / ve));
+        a.tpw_ok = (B * N) % MBRT_GATE_TPW == 0 ? 1 : 0;
         with_dt(attn_dtype, [&](auto at) {
             with_dt(gate_dtype, [&](auto gt) {
                 with_dt(out_dtype, [&](auto ot) {

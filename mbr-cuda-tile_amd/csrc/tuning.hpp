@@ -118,8 +118,8 @@
 #ifndef MBRT_ATTN_HEADS_NT
 #define MBRT_ATTN_HEADS_NT 3  // persistent attention over short heads: non-temporal output stores (bit 0) and K/V/Q loads (bit 1)
 #endif
-#ifndef MBRT_GATE_INORDER
-#define MBRT_GATE_INORDER 0  // gate merge of a head-major [B,H,N,D] input: threads in input order (1) or output order (0)
+#ifndef MBRT_GATE_TPW
+#define MBRT_GATE_TPW 4  // gate merge of a head-major [B,H,N,D] input: tokens per run (1: a block step writes whole token rows; measured 4 > 12, 6, 2, 1 by 1 %)
 #endif
 #ifndef MBRT_ACT_U
 #define MBRT_ACT_U 2     // 16-byte groups per thread: bias + activation (GELU)
