@@ -237,6 +237,77 @@ __global__ __launch_bounds__(kThreads) void softmax_staged_kernel(SmArgs a) {
     }
 }
 
+// Rows of 33..64 two-byte elements, `cols` a multiple of 4, the same dtype in and out:
+// a pair of rows is cols/4 16-byte vectors (at most 16) and starts 16-byte aligned, so one
+// 16-lane group moves it straight between HBM and registers, lane i holding vector i
+// (elements 8i..8i+7 of the pair).  Each 4-element half of a lane's vector then lies in
+// one row; a lane reduces its halves, and the group reduces a max and a sum per row with
+// the 16-lane DPP steps, each half contributing to its own row.  No LDS, no barrier.
+// Lanes past the pair's last vector load that vector again (every load is issued before
+// the first use) and store nothing; groups past the last pair re-read it and store
+// nothing.  In-place calls are safe: a vector is written only by the lane that read it,
+// after every load of its wave.
+template <int DT, int U>
+__global__ __launch_bounds__(kThreads) void softmax_pair_kernel(SmArgs a) {
+    constexpr int kGroups = kThreads / 16;
+    const int i = threadIdx.x & 15;
+    const int nv = a.cols >> 2;  // vectors per pair
+    const int64_t pairs = a.rows >> 1;
+    const int vi = min(i, nv - 1);
+    const bool lane_ok = i < nv;
+    const bool rowA = 8 * i < a.cols, rowB = 8 * i + 4 < a.cols;  // half in the pair's first row
+    // chunks of kGroups * U pairs; a grid smaller than the chunk count walks them
+    const int64_t chunks = (pairs + kGroups * U - 1) / (kGroups * U);
+    for (int64_t chunk = blockIdx.x; chunk < chunks; chunk += gridDim.x) {
+    const int64_t p0 = chunk * (kGroups * U) + (threadIdx.x >> 4);
+    Vec<DT, 8> x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t p = min(p0 + u * kGroups, pairs - 1);
+        x[u].template load<MBRT_NT_SMP>(a.in, (p * nv + vi) * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        float z[8];
+        x[u].to_f32(z);
+        float hA = -INFINITY, hB = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            z[j] *= a.scale_log2e;
+            z[j + 4] *= a.scale_log2e;
+            hA = fmaxf(hA, z[j]);
+            hB = fmaxf(hB, z[j + 4]);
+        }
+        float m0 = fmaxf(rowA ? hA : -INFINITY, rowB ? hB : -INFINITY);
+        float m1 = lane_ok ? fmaxf(rowA ? -INFINITY : hA, rowB ? -INFINITY : hB) : -INFINITY;
+        m0 = group_max<16>(m0);
+        m1 = group_max<16>(m1);
+        const float mA = rowA ? m0 : m1, mB = rowB ? m0 : m1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            z[j] = __builtin_amdgcn_exp2f(z[j] - mA);
+            z[j + 4] = __builtin_amdgcn_exp2f(z[j + 4] - mB);
+        }
+        const float sA = (z[0] + z[1]) + (z[2] + z[3]), sB = (z[4] + z[5]) + (z[6] + z[7]);
+        float s0 = (rowA ? sA : 0.0f) + (rowB ? sB : 0.0f);
+        float s1 = lane_ok ? (rowA ? 0.0f : sA) + (rowB ? 0.0f : sB) : 0.0f;
+        s0 = group_sum<16>(s0);
+        s1 = group_sum<16>(s1);
+        const float inv0 = MBRT_SM_PAIR_RCP ? __builtin_amdgcn_rcpf(s0) : 1.0f / s0;
+        const float inv1 = MBRT_SM_PAIR_RCP ? __builtin_amdgcn_rcpf(s1) : 1.0f / s1;
+        const float iA = rowA ? inv0 : inv1, iB = rowB ? inv0 : inv1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            z[j] *= iA;
+            z[j + 4] *= iB;
+        }
+        x[u].from_f32(z);
+        const int64_t p = p0 + u * kGroups;
+        if (p < pairs && lane_ok) x[u].template store<MBRT_NT_SMP>(a.out, (p * nv + i) * 8);
+    }
+    }
+}
+
 // Long rows: one wave per row, three passes (max, sum, write) over global memory.
 __global__ __launch_bounds__(kThreads) void softmax_loop_kernel(SmArgs a, int idt, int fb) {
     const int lane = threadIdx.x % 64;
@@ -299,6 +370,16 @@ bool launch_short(const SmArgs& a, int in_esize, int out_esize, bool fb, hipStre
     // MBRT_SM_SHORT_BYTES of input its fixed cost dominates, so each group takes
     // MBRT_SM_SHORT_RPG rows
     const bool two = 32 * c * in_esize < MBRT_SM_SHORT_BYTES;
+    if constexpr (IDT != F32) {
+        if (MBRT_SM_PAIR_U > 0 && !fb && out_esize == 2 && a.odt == IDT && c > 32 && c <= 64 && c % 4 == 0 &&
+            a.rows % 2 == 0) {
+            constexpr int U = MBRT_SM_PAIR_U > 0 ? MBRT_SM_PAIR_U : 1;
+            dim3 grid((unsigned)ceil_div(a.rows / 2, (int64_t)(kThreads / 16) * U));
+            if (MBRT_SM_PAIR_BPC > 0) grid.x = (unsigned)std::min<int64_t>(grid.x, (int64_t)cu_count() * MBRT_SM_PAIR_BPC);
+            hipLaunchKernelGGL((softmax_pair_kernel<IDT, U>), grid, dim3(kThreads), 0, st, a);
+            return true;
+        }
+    }
     if (c <= 16 && fits(64)) launch_staged<IDT, 4, 4>(a, fb, st);
     else if (c <= 32 && fits(32)) launch_staged<IDT, 8, 4>(a, fb, st);
     else if (c <= 64 && two && fits(32 * MBRT_SM_SHORT_RPG)) launch_staged<IDT, 8, 8, MBRT_SM_SHORT_RPG>(a, fb, st);

@@ -106,6 +106,18 @@
 #ifndef MBRT_SM_DMA
 #define MBRT_SM_DMA 1  // staged softmax: raw spans loaded straight into LDS (direct-to-LDS loads)
 #endif
+#ifndef MBRT_SM_PAIR_U
+#define MBRT_SM_PAIR_U 1  // 2-byte softmax rows of 33..64 (cols % 4 == 0, even row count): row pairs per 16-lane group from registers (0: LDS-staged kernel)
+#endif
+#ifndef MBRT_NT_SMP
+#define MBRT_NT_SMP 3    // softmax row pairs from registers: non-temporal loads (bit 0) and stores (bit 1)
+#endif
+#ifndef MBRT_SM_PAIR_RCP
+#define MBRT_SM_PAIR_RCP 1  // softmax row pairs: 1/sum as v_rcp_f32 (1) or the correctly rounded division (0)
+#endif
+#ifndef MBRT_SM_PAIR_BPC
+#define MBRT_SM_PAIR_BPC 24  // softmax row pairs: blocks per CU of a grid that walks the chunks (0: one chunk per block)
+#endif
 #ifndef MBRT_SM_SHORT_RPG
 #define MBRT_SM_SHORT_RPG 2  // rows per lane group in those blocks
 #endif

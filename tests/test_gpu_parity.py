@@ -456,7 +456,26 @@ def test_softmax_short_rows(orc, dev, rows, cols, idt, odt):
         assert_bitexact(to_host(xd, odt), to_host(y, odt), "softmax short in place")
 
 
-@pytest.mark.parametrize("rows,cols", [(96, 801), (96, 60), (96, 16), (23, 801), (23, 60), (5, 3000)])
+@pytest.mark.parametrize("cols", [36, 40, 44, 52, 56, 60, 64])
+@pytest.mark.parametrize("rows", [2, 34, 1000, 6406])
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_softmax_row_pairs(orc, dev, rows, cols, dt):
+    """Two-byte rows of 33..64 columns (a multiple of 4) in an even count: the register
+    kernel that gives each pair of rows to 16 lanes, where a lane's 8 elements may straddle
+    the two rows (cols = 4 mod 8).  Then the same call in place."""
+    say(f"softmax row pairs rows={rows} cols={cols} dt={dt}")
+    x = inp(orc, (rows, cols), 43, cols, dt, std=4.0)
+    xd = to_dev(x, dt)
+    y = empty((rows, cols), dt)
+    mbrt.softmax(xd, y, 0.7)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, dt), orc.softmax(x, dt, dt, 0.7), dt, "softmax row pairs")
+    mbrt.softmax(xd, xd, 0.7)
+    torch.cuda.synchronize()
+    assert_bitexact(to_host(xd, dt), to_host(y, dt), "softmax row pairs in place")
+
+
+@pytest.mark.parametrize("rows,cols", [(96, 801), (96, 60), (96, 16), (23, 801), (23, 60), (5, 3000), (96, 44)])
 @pytest.mark.parametrize("dt", [F32, BF16])
 def test_softmax_special_values(orc, dev, rows, cols, dt):
     """Masked scores on every softmax path (LDS-staged long and short rows, the unaligned
