@@ -127,7 +127,9 @@ def build_ops(torch, mbrt, bands):
             op = Op(f"bl3_softmax_{tag}_{dname}", 2 * rows * cols * es,
                     (lambda rows=rows, cols=cols, dt=dt: dict(x=randn((rows, cols), dt, 3.0),
                                                               y=torch.empty((rows, cols), dtype=dt, device=dev))),
-                    "softmax_staged_kernel")  # rows of up to 1024 elements are staged through LDS
+                    # rows of up to 1024 elements are staged through LDS; 2-byte rows of 60 go
+                    # in register row pairs
+                    "softmax_pair_kernel" if (tag, dname) == ("freq", "bf16") else "softmax_staged_kernel")
             op.run = lambda b: mbrt.softmax(b["x"], b["y"], 1.0)
             ops.append(op)
 
