@@ -380,9 +380,12 @@ def test_gate_merge_bl2c_full(orc, dev):
 
 @pytest.mark.parametrize("D,adt,gdt,odt,logit", [(64, F32, F32, F32, True), (12, BF16, F32, BF16, True),
                                                  (16, F32, BF16, F32, False), (64, F16, F16, F16, True)])
-def test_gate_merge_variants(orc, dev, D, adt, gdt, odt, logit):
-    say(f"gate merge D={D}")
-    B, H, N = 3, 4, 19
+@pytest.mark.parametrize("B,N", [(3, 19), (4, 21)])
+def test_gate_merge_variants(orc, dev, D, adt, gdt, odt, logit, B, N):
+    """B*N = 57 takes the token-row order of the head-major input; B*N = 84, a multiple
+    of 4, the order that walks 4 tokens x all heads per step."""
+    say(f"gate merge D={D} B={B} N={N}")
+    H = 4
     attn = inp(orc, (B, H, N, D), 25, D, adt)
     gate = inp(orc, (B, N, H), 26, D, gdt, std=2.0)
     y = empty((B, N, H * D), odt)
