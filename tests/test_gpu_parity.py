@@ -397,13 +397,26 @@ def test_gate_merge_variants(orc, dev, D, adt, gdt, odt, logit, B, N):
 
 # ---- softmax -------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("shape", [(480, 801, 801), (6408, 60, 60)])
+_bl3_cache = {}
+
+
+def _bl3_input(orc, rows, cols):
+    """The f32 draw of one BL-3 shape (308M values for the time shape), made once for both
+    dtypes."""
+    if (rows, cols) not in _bl3_cache:
+        _bl3_cache.clear()
+        _bl3_cache[(rows, cols)] = orc.randn((rows, cols), seed=SEED[3], stream=0, std=3.0)
+    return _bl3_cache[(rows, cols)]
+
+
 @pytest.mark.parametrize("dt", [F32, BF16])
+@pytest.mark.parametrize("shape", [(480, 801, 801), (6408, 60, 60)])
 def test_softmax_bl3_full(orc, dev, shape, dt):
     say(f"BL-3 softmax {shape} dt={dt}")
     rows, cols = shape[0] * shape[1], shape[2]
-    g = torch.Generator(device="cuda").manual_seed(SEED[3])
-    x = (torch.randn((rows, cols), generator=g, device="cuda") * 3.0).to(torch.float32 if dt == F32 else torch.bfloat16)
+    # the configuration's own inputs: N(0, 3) from the BL-3 stream, rounded to the dtype
+    x32 = _bl3_input(orc, rows, cols)
+    x = to_dev(x32 if dt == F32 else orc.from_f32(x32, dt), dt)
     y = torch.empty_like(x)
     mbrt.softmax(x, y, 1.0)
     torch.cuda.synchronize()
