@@ -1,6 +1,8 @@
-"""Seeded random-shape parity sweep of the widened entry points: the fused attention in its
-strided / q-rotary / gated forms, the attention with n_q != n_k, and the STFT / iSTFT over
-random lengths, hops, centring, normalisation and windows.  Every case is drawn from a
+"""Seeded random-shape parity sweep: the row softmax, the sigmoid gate merge, RMSNorm and
+GLU over random shapes, dtypes and layouts (every kernel form their launchers pick), and
+the widened entry points: the fused attention in its strided / q-rotary / gated forms, the
+attention with n_q != n_k, and the STFT / iSTFT over random lengths, hops, centring,
+normalisation and windows.  Every case is drawn from a
 fixed seed at import, so a failure names a reproducible shape; the sizes stay small
 enough for the float64 oracle.
 
@@ -17,7 +19,7 @@ import torch
 
 import mbrt
 from gpu_util import empty, say, to_dev, to_host
-from parity import BF16, F32, assert_bitexact, assert_close
+from parity import BF16, F16, F32, assert_bitexact, assert_close
 
 pytestmark = pytest.mark.gpu
 
@@ -45,10 +47,93 @@ def _cases():
 
 ATTN_CASES, CROSS_CASES, STFT_CASES = _cases()
 
+SM_DTYPES = [(F32, F32), (BF16, BF16), (F32, BF16), (BF16, F32), (F16, F16)]
+
+
+def _op_cases():
+    rng = np.random.default_rng(0x4D425210)
+    pick = lambda lo, hi: int(rng.integers(lo, hi))  # noqa: E731
+    # row counts and lengths spread over every softmax form: short rows in groups of 4-16
+    # lanes, the 2-byte row pairs (33..64, a multiple of 4, even row counts), the staged
+    # spans of 129..1024 and the unaligned and long-row kernels
+    softmax = []
+    for _ in range(24):
+        cols = [pick(1, 33), 4 * pick(9, 17), pick(33, 129), pick(129, 1025), pick(1025, 3000)][pick(0, 5)]
+        rows = pick(1, 2500) * [1, 2][pick(0, 2)]
+        softmax.append((rows, cols, SM_DTYPES[pick(0, 5)], round(float(rng.uniform(0.05, 2.0)), 3)))
+    gate = [(pick(1, 5), pick(1, 10), pick(1, 200), [4, 5, 8, 12, 16, 32, 64, 128][pick(0, 8)],
+             [(BF16, BF16, BF16), (F32, F32, F32), (BF16, F32, BF16), (F16, F16, F16), (BF16, BF16, F32)][pick(0, 5)],
+             bool(pick(0, 2)), bool(pick(0, 2))) for _ in range(12)]
+    rms = [(pick(1, 400), pick(1, 5000), [(F32, F32, F32), (BF16, F32, BF16), (BF16, BF16, BF16), (F16, F32, F16)][pick(0, 4)])
+           for _ in range(8)]
+    glu = [(pick(1, 300), pick(1, 700), [(F32, F32), (BF16, BF16), (F32, BF16), (F16, F16)][pick(0, 4)])
+           for _ in range(8)]
+    return softmax, gate, rms, glu
+
+
+SM_CASES, GATE_CASES, RMS_CASES, GLU_CASES = _op_cases()
+
 
 def _inp(orc, shape, seed, stream, dt, std=1.0):
     x = orc.randn(shape, seed=seed, stream=stream, std=std)
     return x if dt == F32 else orc.from_f32(x, dt)
+
+
+@pytest.mark.parametrize("rows,cols,dts,scale", SM_CASES)
+def test_random_softmax(orc, dev, rows, cols, dts, scale):
+    idt, odt = dts
+    say(f"random softmax rows={rows} cols={cols} {idt}->{odt} scale={scale}")
+    x = _inp(orc, (rows, cols), 0x4D425200D1, rows * 7 + cols, idt, std=3.0)
+    xd = to_dev(x, idt)
+    y = empty((rows, cols), odt)
+    mbrt.softmax(xd, y, scale)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), orc.softmax(x, idt, odt, scale), odt, "softmax")
+    if idt == odt:
+        mbrt.softmax(xd, xd, scale)
+        torch.cuda.synchronize()
+        assert_bitexact(to_host(xd, odt), to_host(y, odt), "softmax in place")
+
+
+@pytest.mark.parametrize("B,H,N,D,dts,logit,bnhd", GATE_CASES)
+def test_random_gate_merge(orc, dev, B, H, N, D, dts, logit, bnhd):
+    adt, gdt, odt = dts
+    say(f"random gate merge B={B} H={H} N={N} D={D} {adt},{gdt}->{odt} logit={logit} bnhd={bnhd}")
+    attn = _inp(orc, (B, H, N, D), 0x4D425200D2, N * 13 + D, adt)
+    gate = _inp(orc, (B, N, H), 0x4D425200D3, N * 13 + D, gdt, std=2.0)
+    ref = orc.gate_merge(attn, adt, gate, gdt, odt, B, H, N, D, layout=0, logit=logit)
+    y = empty((B, N, H * D), odt)
+    if bnhd:
+        mbrt.gate_merge(to_dev(np.ascontiguousarray(attn.transpose(0, 2, 1, 3)), adt), to_dev(gate, gdt), y,
+                        mbrt.LAYOUT_BNHD, gate_is_logit=logit)
+    else:
+        mbrt.gate_merge(to_dev(attn, adt), to_dev(gate, gdt), y, mbrt.LAYOUT_BHND, gate_is_logit=logit)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), ref, odt, "gate merge")
+
+
+@pytest.mark.parametrize("rows,D,dts", RMS_CASES)
+def test_random_rmsnorm(orc, dev, rows, D, dts):
+    xdt, gdt, odt = dts
+    say(f"random rms_norm rows={rows} D={D} {xdt},{gdt}->{odt}")
+    x = _inp(orc, (rows, D), 0x4D425200D4, rows + D, xdt)
+    g = orc.randn((D,), seed=0x4D425200D5, stream=D, mean=1.0, std=0.02)
+    g = g if gdt == F32 else orc.from_f32(g, gdt)
+    y = empty((rows, D), odt)
+    mbrt.rms_norm(to_dev(x, xdt), to_dev(g, gdt), y, scale=float(np.sqrt(D)), eps=1e-8)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), orc.rms_norm(x, xdt, g, gdt, odt, float(np.sqrt(D)), 1e-8), odt, "rms")
+
+
+@pytest.mark.parametrize("rows,half,dts", GLU_CASES)
+def test_random_glu(orc, dev, rows, half, dts):
+    xdt, odt = dts
+    say(f"random glu rows={rows} half={half} {xdt}->{odt}")
+    x = _inp(orc, (rows, 2 * half), 0x4D425200D6, rows + half, xdt, std=1.5)
+    y = empty((rows, half), odt)
+    mbrt.glu(to_dev(x, xdt), y)
+    torch.cuda.synchronize()
+    assert_close(to_host(y, odt), orc.glu(x, xdt, odt), odt, "glu")
 
 
 @pytest.mark.parametrize("B,N,H,rot,gate,odt,tdt", ATTN_CASES)
