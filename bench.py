@@ -490,7 +490,7 @@ def cpu_baseline(threads: int | None):
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+        print(f"bench.py: measures one GPU only (got --gpus {args.gpus}); "
               "the ops shard per row with no exchange, so run one process per GPU.", file=sys.stderr)
         sys.exit(2)
     import torch

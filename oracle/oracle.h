@@ -1,9 +1,9 @@
 /*
  * oracle.h — CPU restatement of the reference's tensor-op semantics.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker for the GPU kernels in
- * mbr-cuda-tile_amd/: it is loaded by tests/, by __graft_entry__.smoke() and by the
- * cpu_baseline leg of bench.py, and nothing in the product links or calls it.
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle that the GPU kernels in
+ * mbr-cuda-tile_amd/ are held to: it is loaded by tests/, by __graft_entry__.smoke() and
+ * by the cpu_baseline leg of bench.py, and nothing in the product links or calls it.
  *
  * Every op is plain host C++ over host buffers, with dtype codes equal to the C-ABI's
  * (F32=0, F16=1, I64=2, BF16=3, I32=4).  Float ops take `mode`:

@@ -1,5 +1,5 @@
-"""numpy wrapper of liboracle.so — TEST INFRASTRUCTURE ONLY (the checker of the GPU
-kernels; see oracle.h).  Only tests/, __graft_entry__.smoke() and bench.py's
+"""numpy wrapper of liboracle.so — TEST INFRASTRUCTURE ONLY (the oracle the GPU kernels
+are held to; see oracle.h).  Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg import it.
 
 Storage conventions: f32 -> np.float32; bf16 and f16 -> np.uint16 bit patterns;
